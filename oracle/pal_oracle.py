@@ -1,0 +1,358 @@
+"""CPU oracle for PAL's paged-attention path -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The shipped operators in ``proxy_attention_lab`` run exclusively on
+the HIP library and fail loudly when it is missing.
+
+It restates, in numpy, what the reference computes on the hot path:
+
+* ``fill_kv_pages``        -- kernels/paged_attention/fill_kv_pages.h.metal:56-116
+  (index math) and src/fill_kv_pages_primitive.cpp:91-92 (functional copy).
+* ``paged_attention_decode`` -- kernels/paged_attention/decode/
+  paged_attention_decode.h.metal:59-65 (GQA map), :106-116 (1/sqrt(HD) scale),
+  :125-131 and :298-306 (length mask), :212-241 (softmax), output shape from
+  src/paged_attention_decode_primitive.cpp:289-300.
+* ``paged_attention_decode_two_pass`` -- the 512-token chunking of
+  paged_attention_decode_primitive.cpp:100-102 and decode.h.metal:122-139,
+  367-395, merged as in decode/paged_reduce_decode.h.metal:79-128.
+* ``paged_attention_prefill`` -- prefill/paged_attention_prefill.h.metal:
+  62-74 (row addressing), :147-234 (causal prompt part), :251-360 (paged
+  history part), :368-388 (normalise / write); output shape from
+  src/paged_attention_prefill_primitive.cpp:188-192, uniform prompt length
+  from :115-116.
+* ``paged_attention`` (fused mixed batch) has no reference function; its
+  semantics are defined by this build: row r of sequence s = q2seq[r] attends
+  to the keys [0, min(seq_lens[s], q_offset[r])) of s, all read from pages.
+
+All pools and activations are handled as raw 16-bit patterns (uint16) plus a
+dtype tag ("f16" or "bf16"), so bf16 needs no numpy dtype and fill parity can
+be checked bit for bit.  Attention math runs in float32, the precision the
+reference accumulates in.
+
+Pinning (what checks this oracle, in tests/test_oracle.py):
+  * fill index math: the reference tests' own expected-pool loops
+    (fill_kv_pages/test_fill_*.py), restated as known-answer tests, plus an
+    independent scalar loop;
+  * decode / prefill / fused: torch.nn.functional.scaled_dot_product_attention
+    in float32 on contiguous K/V (a library routine), the closed-form
+    known-answer tests of decode/test_full_attention.py,
+    decode/test_softmax_and_value.py, prefill/test_softmax_and_value.py,
+    invariance under page-table permutation, and a brute-force scalar loop
+    on tiny shapes;
+  * two-pass: equality with the single-pass result (any chunk size).
+The reference's epsilon (+1e-6 in denominators) and -88 exp clamp are not
+reproduced: their relative effect is below 1e-6.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+MEMORY_ALIGNMENT_BYTES = 16  # include/kernels/paged_attention_types.h:37
+CHUNK_SIZE = 512  # include/kernels/paged_attention_types.h:33
+
+# ---------------------------------------------------------------------------
+# 16-bit float helpers
+# ---------------------------------------------------------------------------
+
+
+def bits_to_f32(bits: np.ndarray, dtype: str) -> np.ndarray:
+    """Decode raw fp16/bf16 bit patterns (uint16) into float32."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    if dtype == "f16":
+        return bits.view(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        return (bits.astype(np.uint32) << 16).view(np.float32)
+    raise ValueError(f"unsupported dtype {dtype!r}")
+
+
+def f32_to_bits(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 to fp16/bf16 (round to nearest even) and return the bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == "f16":
+        with np.errstate(over="ignore"):  # out-of-range values become +-inf, as in a cast
+            return x.astype(np.float16).view(np.uint16)
+    if dtype == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        nan = np.isnan(x)
+        if nan.any():
+            rounded = rounded.copy()
+            rounded[nan] = 0x7FC0
+        return rounded
+    raise ValueError(f"unsupported dtype {dtype!r}")
+
+
+def stripe_size(dtype: str) -> int:
+    """K-cache stripe width x = 16 / sizeof(T) (bindings.cpp:44-48)."""
+    if dtype not in ("f16", "bf16"):
+        raise ValueError(f"unsupported dtype {dtype!r}")
+    return MEMORY_ALIGNMENT_BYTES // 2
+
+
+# ---------------------------------------------------------------------------
+# fill_kv_pages
+# ---------------------------------------------------------------------------
+
+
+def fill_kv_pages(new_k, new_v, k_pool, v_pool, page_table, write_pos, q2seq):
+    """Scatter new K/V rows into copies of the pools (bit patterns, uint16).
+
+    new_k/new_v: [N, Hkv, HD] uint16.  k_pool: [P, Hkv, HD/x, TPP, x];
+    v_pool: [P, Hkv, HD, TPP].  Follows fill_kv_pages.h.metal:65-116:
+    seq = q2seq[t], pos = write_pos[t], page = page_table[seq, pos // TPP],
+    slot = pos % TPP, K[page, h, d // x, slot, d % x] = new_k[t, h, d],
+    V[page, h, d, slot] = new_v[t, h, d].  Returns (k_out, v_out); the inputs
+    are left untouched, like the reference's copy at
+    fill_kv_pages_primitive.cpp:91-92.  Duplicate destinations are undefined
+    in the reference (racing writes); here the last token wins.
+    """
+    k_out = np.array(k_pool, dtype=np.uint16, copy=True)
+    v_out = np.array(v_pool, dtype=np.uint16, copy=True)
+    n = int(new_k.shape[0])
+    if n == 0:
+        return k_out, v_out
+    _, hkv, nstripe, tpp, x = k_out.shape
+    hd = nstripe * x
+    pt = np.asarray(page_table).astype(np.int64)
+    seq = np.asarray(q2seq).astype(np.int64)
+    pos = np.asarray(write_pos).astype(np.int64)
+    page = pt[seq, pos // tpp]
+    slot = pos % tpp
+    nk = np.asarray(new_k, dtype=np.uint16).reshape(n, hkv, nstripe, x)
+    nv = np.asarray(new_v, dtype=np.uint16).reshape(n, hkv, hd)
+    for t in range(n):  # sequential order makes the "last writer wins" rule explicit
+        k_out[page[t], :, :, slot[t], :] = nk[t]
+        v_out[page[t], :, :, slot[t]] = nv[t]
+    return k_out, v_out
+
+
+# ---------------------------------------------------------------------------
+# attention helpers
+# ---------------------------------------------------------------------------
+
+
+def gather_tokens(k_pool_f32, v_pool_f32, page_row, n_tokens):
+    """Read tokens [0, n_tokens) of one sequence out of the pools.
+
+    Inverse of the test-side scatter at decode/test_sdpa_equivalency.py:141-173
+    and prefill/test_sdpa_equivalency.py:98-117; the addressing follows
+    decode.h.metal:143-190 (K) and :249-295 (V).  Returns K, V as
+    [n_tokens, Hkv, HD] float32.
+    """
+    _, hkv, nstripe, tpp, x = k_pool_f32.shape
+    hd = nstripe * x
+    if n_tokens <= 0:
+        z = np.zeros((0, hkv, hd), np.float32)
+        return z, z.copy()
+    j = np.arange(n_tokens)
+    pages = np.asarray(page_row).astype(np.int64)[j // tpp]
+    slots = j % tpp
+    # k_pool[page, h, c, slot, e] -> [n, h, c, e] -> [n, h, hd]
+    k = k_pool_f32[pages, :, :, slots, :].reshape(n_tokens, hkv, hd)
+    # v_pool[page, h, d, slot] -> [n, h, d]
+    v = v_pool_f32[pages, :, :, slots]
+    return np.ascontiguousarray(k), np.ascontiguousarray(v)
+
+
+def attend(q, k, v, limits, causal_pos=None):
+    """Softmax attention with GQA for one sequence.
+
+    q: [R, Hq, HD]; k, v: [L, Hkv, HD]; limits: [R] -- row r attends to keys
+    [0, limits[r]).  Scale is 1/sqrt(HD) (decode.h.metal:115,
+    prefill.h.metal:178).  Query head h reads KV head h // (Hq // Hkv)
+    (decode.h.metal:64-65).  Rows with no key produce zeros.
+    Returns [R, Hq, HD] float32.
+    """
+    r_rows, hq, hd = q.shape
+    l_keys, hkv, _ = k.shape
+    g = hq // hkv
+    out = np.zeros((r_rows, hq, hd), np.float32)
+    if r_rows == 0 or l_keys == 0:
+        return out
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    qg = q.reshape(r_rows, hkv, g, hd).transpose(1, 0, 2, 3).reshape(hkv, r_rows * g, hd)
+    kt = k.transpose(1, 2, 0)  # [Hkv, HD, L]
+    s = np.matmul(qg, kt) * scale  # [Hkv, R*G, L]
+    lim = np.repeat(np.asarray(limits, np.int64), g)  # [R*G]
+    mask = np.arange(l_keys)[None, :] >= lim[:, None]
+    s = np.where(mask[None], -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    p = np.exp(s - m)
+    den = p.sum(axis=-1, keepdims=True)
+    o = np.matmul(p, v.transpose(1, 0, 2))  # [Hkv, R*G, HD]
+    o = np.where(den > 0, o / np.where(den > 0, den, 1.0), 0.0)
+    out[:] = o.reshape(hkv, r_rows, g, hd).transpose(1, 0, 2, 3).reshape(r_rows, hq, hd)
+    return out
+
+
+def _pools_f32(k_pool, v_pool, dtype):
+    return bits_to_f32(k_pool, dtype), bits_to_f32(v_pool, dtype)
+
+
+# ---------------------------------------------------------------------------
+# operators
+# ---------------------------------------------------------------------------
+
+
+def paged_attention_decode(queries, k_pool, v_pool, page_table, seq_lens, dtype):
+    """Decode: one query row per sequence over its paged context.
+
+    queries: [N, Hq, HD] (or [N, HD] meaning Hq = 1) uint16 bits, N >= S; row s
+    serves sequence s and rows >= S are ignored (decode.h.metal:106-108).
+    Returns [S, Hq, HD] float32 (decode_primitive.cpp:289-300).
+    """
+    q = bits_to_f32(queries, dtype)
+    if q.ndim == 2:
+        q = q[:, None, :]
+    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    s_count = int(np.asarray(page_table).shape[0])
+    hq, hd = q.shape[1], q.shape[2]
+    out = np.zeros((s_count, hq, hd), np.float32)
+    lens = np.asarray(seq_lens).astype(np.int64)
+    for s in range(s_count):
+        n = int(lens[s])
+        k, v = gather_tokens(kf, vf, np.asarray(page_table)[s], n)
+        out[s] = attend(q[s : s + 1], k, v, [n])[0]
+    return out
+
+
+def paged_attention_decode_two_pass(queries, k_pool, v_pool, page_table, seq_lens, dtype,
+                                    chunk_size=CHUNK_SIZE):
+    """Decode computed chunk by chunk and merged with a log-sum-exp reduction.
+
+    Pass 1 (decode.h.metal:122-139, 211-241, 367-395): chunk c covers tokens
+    [c*chunk, (c+1)*chunk); it yields the chunk max m_c, the chunk exp-sum l_c
+    and the chunk-normalised output o_c.  Pass 2 (paged_reduce_decode.h.metal:
+    79-128): M = max_c m_c, w_c = l_c * exp(m_c - M),
+    out = sum_c w_c * o_c / sum_c w_c.  Returns [S, Hq, HD] float32.
+    """
+    q = bits_to_f32(queries, dtype)
+    if q.ndim == 2:
+        q = q[:, None, :]
+    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    s_count = int(np.asarray(page_table).shape[0])
+    hq, hd = q.shape[1], q.shape[2]
+    hkv = kf.shape[1]
+    g = hq // hkv
+    scale = np.float32(1.0 / np.sqrt(np.float32(hd)))
+    out = np.zeros((s_count, hq, hd), np.float32)
+    lens = np.asarray(seq_lens).astype(np.int64)
+    for s in range(s_count):
+        n = int(lens[s])
+        if n <= 0:
+            continue
+        k, v = gather_tokens(kf, vf, np.asarray(page_table)[s], n)
+        qs = q[s].reshape(hkv, g, hd)
+        ms, ls, os_ = [], [], []
+        for c0 in range(0, n, chunk_size):
+            kc = k[c0 : c0 + chunk_size].transpose(1, 2, 0)  # [Hkv, HD, Lc]
+            vc = v[c0 : c0 + chunk_size].transpose(1, 0, 2)  # [Hkv, Lc, HD]
+            sc = np.matmul(qs, kc) * scale  # [Hkv, G, Lc]
+            m = sc.max(axis=-1, keepdims=True)
+            p = np.exp(sc - m)
+            l_c = p.sum(axis=-1, keepdims=True)
+            ms.append(m)
+            ls.append(l_c)
+            os_.append(np.matmul(p, vc) / l_c)
+        m_all = np.stack(ms)  # [C, Hkv, G, 1]
+        big_m = m_all.max(axis=0)
+        w = np.stack(ls) * np.exp(m_all - big_m)
+        o = (w * np.stack(os_)).sum(axis=0) / w.sum(axis=0)
+        out[s] = o.reshape(hq, hd)
+    return out
+
+
+def paged_attention_prefill(q_prompt, k_prompt, v_prompt, k_pool, v_pool, page_table,
+                            context_lens, dtype):
+    """Prefill over paged history plus a causal dense prompt.
+
+    q_prompt: [S*P, Hq, HD]; k_prompt/v_prompt: [S*P, Hkv, HD]; P is uniform,
+    P = q_prompt.shape[0] // S (prefill_primitive.cpp:115-116).  Prompt token
+    i of sequence s (global row s*P + i) attends to all context_lens[s]
+    history tokens read from pages (prefill.h.metal:251-360) and to prompt
+    tokens j <= i (prefill.h.metal:147-165).  Returns [S*P*Hq, HD] float32
+    with row (s*P + i)*Hq + h (prefill.h.metal:379-381).
+    """
+    q = bits_to_f32(q_prompt, dtype)
+    kp = bits_to_f32(k_prompt, dtype)
+    vp = bits_to_f32(v_prompt, dtype)
+    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    pt = np.asarray(page_table)
+    s_count = int(pt.shape[0])
+    rows, hq, hd = q.shape
+    p_len = rows // s_count if s_count else 0
+    out = np.zeros((rows, hq, hd), np.float32)
+    hist = np.asarray(context_lens).astype(np.int64)
+    for s in range(s_count):
+        h_len = int(hist[s])
+        kh, vh = gather_tokens(kf, vf, pt[s], h_len)
+        sl = slice(s * p_len, (s + 1) * p_len)
+        k = np.concatenate([kh, kp[sl]], axis=0)
+        v = np.concatenate([vh, vp[sl]], axis=0)
+        limits = h_len + np.arange(1, p_len + 1)
+        out[sl] = attend(q[sl], k, v, limits)
+    return out.reshape(rows * hq, hd)
+
+
+def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offset, dtype):
+    """Fused mixed batch (build-defined; no reference function exists).
+
+    Row r belongs to sequence s = q2seq[r] and attends to the keys
+    [0, min(seq_lens[s], q_offset[r])) of s, all read from pages.  A decode
+    row uses q_offset = seq_lens[s]; a prefill row at absolute position p uses
+    q_offset = p + 1.  Returns [R, Hq, HD] float32.
+    """
+    q = bits_to_f32(queries, dtype)
+    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    pt = np.asarray(page_table)
+    lens = np.asarray(seq_lens).astype(np.int64)
+    seqs = np.asarray(q2seq).astype(np.int64)
+    offs = np.asarray(q_offset).astype(np.int64)
+    out = np.zeros(q.shape, np.float32)
+    for s in np.unique(seqs):
+        rows = np.nonzero(seqs == s)[0]
+        limits = np.minimum(lens[s], offs[rows])
+        n = int(max(0, limits.max()))
+        k, v = gather_tokens(kf, vf, pt[s], n)
+        out[rows] = attend(q[rows], k, v, limits)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# layout helpers (restated for the tests; the product has its own)
+# ---------------------------------------------------------------------------
+
+
+def k_cache_shape(num_pages, num_kv_heads, head_dim, tokens_per_page, dtype):
+    """decode_primitive.cpp:384-397."""
+    x = stripe_size(dtype)
+    return (num_pages, num_kv_heads, head_dim // x, tokens_per_page, x)
+
+
+def v_cache_shape(num_pages, num_kv_heads, head_dim, tokens_per_page, dtype):
+    """decode_primitive.cpp:373-381."""
+    stripe_size(dtype)
+    return (num_pages, num_kv_heads, head_dim, tokens_per_page)
+
+
+def scatter_contiguous(k_seq, v_seq, k_pool, v_pool, page_row):
+    """Write contiguous per-sequence K/V [L, Hkv, HD] (bits) into pools in place.
+
+    The reshape/transpose formulation of the reference tests
+    (decode/test_sdpa_equivalency.py:141-173): K tokens of page p are
+    reshaped to [count, HD/x, x] and transposed to [HD/x, count, x]; V is
+    written transposed as [HD, count].
+    """
+    _, hkv, nstripe, tpp, x = k_pool.shape
+    n = k_seq.shape[0]
+    for lp in range((n + tpp - 1) // tpp):
+        page = int(page_row[lp])
+        t0, t1 = lp * tpp, min((lp + 1) * tpp, n)
+        cnt = t1 - t0
+        for h in range(hkv):
+            ks = k_seq[t0:t1, h, :].reshape(cnt, nstripe, x).transpose(1, 0, 2)
+            k_pool[page, h, :, :cnt, :] = ks
+            v_pool[page, h, :, :cnt] = v_seq[t0:t1, h, :].T

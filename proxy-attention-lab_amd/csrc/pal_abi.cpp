@@ -1,0 +1,214 @@
+// C ABI of libpal_hip.so: argument validation, workspace sizing and launch.
+//
+// Replaces the reference's binding + primitive host layers
+// (src/pal_core/bindings.cpp, src/pal_core/src/ops.cpp,
+// src/pal_core/src/*_primitive.cpp).  The library is stateless apart from a
+// thread-local error message; it never allocates device memory.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/pal_hip.h"
+#include "pal_hip_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return PAL_OK;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return ok();
+  return fail(PAL_ERR_HIP, "[%s] HIP error: %s", what, hipGetErrorString(err));
+}
+
+bool valid_dtype(int dtype) { return dtype == PAL_DTYPE_FLOAT16 || dtype == PAL_DTYPE_BFLOAT16; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool decode_head_dim_supported(int hd) {
+  return hd == 32 || hd == 64 || hd == 80 || hd == 96 || hd == 128 || hd == 256;
+}
+
+// Partition size (tokens) -> 16-token blocks per wavefront (4 wavefronts).
+int blocks_per_wave_for(int partition_size) {
+  switch (partition_size) {
+    case 0: return 8;  // default: the reference's CHUNK_SIZE of 512 tokens
+    case 128: return 2;
+    case 256: return 4;
+    case 512: return 8;
+    default: return -1;
+  }
+}
+
+int64_t decode_max_parts(int64_t page_table_width, int tokens_per_page, int bpw) {
+  const int64_t blocks = (page_table_width * tokens_per_page + 15) / 16;
+  const int64_t per_part = 4LL * bpw;
+  return (blocks + per_part - 1) / per_part;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pal_last_error(void) { return g_last_error.c_str(); }
+
+const char* pal_version(void) { return "2025.06.4+gfx950"; }
+
+int pal_get_k_cache_stripe_size(int dtype) {
+  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
+  ok();
+  return 16 / 2;
+}
+
+int pal_get_optimal_page_size(void) { return 16; }
+
+int pal_get_k_cache_shape(int64_t num_pages, int num_kv_heads, int head_dim, int tokens_per_page,
+                          int dtype, int64_t out_shape[5]) {
+  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
+  const int x = 8;
+  out_shape[0] = num_pages;
+  out_shape[1] = num_kv_heads;
+  out_shape[2] = head_dim / x;
+  out_shape[3] = tokens_per_page;
+  out_shape[4] = x;
+  return ok();
+}
+
+int pal_get_v_cache_shape(int64_t num_pages, int num_kv_heads, int head_dim, int tokens_per_page,
+                          int dtype, int64_t out_shape[4]) {
+  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
+  out_shape[0] = num_pages;
+  out_shape[1] = num_kv_heads;
+  out_shape[2] = head_dim;
+  out_shape[3] = tokens_per_page;
+  return ok();
+}
+
+int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool, void* v_pool,
+                      const uint32_t* page_table, const int32_t* write_positions,
+                      const uint32_t* query_to_seq_map, int dtype, int64_t num_tokens,
+                      int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                      int64_t num_seqs, int64_t page_table_width, void* stream) {
+  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] unsupported dtype code %d", dtype);
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
+      num_pages < 0 || num_seqs < 0 || page_table_width < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] negative or zero dimension");
+  if (head_dim % 8 != 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] head_dim %d must be a multiple of 8", head_dim);
+  if (num_tokens == 0) return ok();
+  if (!new_keys || !new_values || !k_pool || !v_pool || !page_table || !write_positions || !query_to_seq_map)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] null pointer argument");
+  if (!aligned16(new_keys) || !aligned16(new_values) || !aligned16(k_pool))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] new_keys, new_values and k_pool must be 16-byte aligned");
+  pal::FillParams p;
+  p.new_k = static_cast<const uint16_t*>(new_keys);
+  p.new_v = static_cast<const uint16_t*>(new_values);
+  p.k_pool = static_cast<uint16_t*>(k_pool);
+  p.v_pool = static_cast<uint16_t*>(v_pool);
+  p.page_table = page_table;
+  p.write_pos = write_positions;
+  p.q2seq = query_to_seq_map;
+  p.num_tokens = num_tokens;
+  p.num_pages = num_pages;
+  p.num_seqs = num_seqs;
+  p.page_table_width = page_table_width;
+  p.num_kv_heads = num_kv_heads;
+  p.head_dim = head_dim;
+  p.tokens_per_page = tokens_per_page;
+  return hip_status(pal::launch_fill_kv_pages(p, static_cast<hipStream_t>(stream)), "fill_kv_pages");
+}
+
+size_t pal_paged_attention_decode_workspace_size(int64_t num_seqs, int num_q_heads, int head_dim,
+                                                 int tokens_per_page, int64_t page_table_width,
+                                                 int partition_size) {
+  const int bpw = blocks_per_wave_for(partition_size);
+  if (bpw < 0 || num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
+      page_table_width <= 0)
+    return 0;
+  const int64_t parts = decode_max_parts(page_table_width, tokens_per_page, bpw);
+  if (parts <= 1) return 0;
+  const int64_t slots = num_seqs * num_q_heads * parts;
+  return static_cast<size_t>(slots) * (static_cast<size_t>(head_dim) + 2) * sizeof(float);
+}
+
+int pal_paged_attention_decode(const void* queries, const void* k_pool, const void* v_pool,
+                               const uint32_t* page_table, const int32_t* sequence_lengths,
+                               void* out, int dtype, int64_t num_query_rows, int64_t num_seqs,
+                               int num_q_heads, int num_kv_heads, int head_dim,
+                               int tokens_per_page, int64_t num_pages, int64_t page_table_width,
+                               int partition_size, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (!valid_dtype(dtype))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] unsupported dtype code %d", dtype);
+  if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
+      num_pages < 0 || page_table_width < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] negative or zero dimension");
+  if (num_q_heads % num_kv_heads != 0)
+    return fail(PAL_ERR_RUNTIME, "num_q_heads must be divisible by num_kv_heads (%d %% %d != 0)",
+                num_q_heads, num_kv_heads);
+  if (!decode_head_dim_supported(head_dim))
+    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for head_dim %d (supported: 32, 64, 80, 96, 128, 256)", head_dim);
+  if (tokens_per_page != 16 && tokens_per_page != 32)
+    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for tokens_per_page %d (supported: 16, 32)", tokens_per_page);
+  const int bpw = blocks_per_wave_for(partition_size);
+  if (bpw < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] partition_size %d not in {0, 128, 256, 512}", partition_size);
+  if (num_query_rows < num_seqs)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] %lld query rows for %lld sequences",
+                static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs));
+  if (num_seqs == 0) return ok();
+  if (num_seqs > 65535)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] at most 65535 sequences per call");
+  if (!queries || !k_pool || !v_pool || !sequence_lengths || !out || (page_table_width > 0 && !page_table))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] null pointer argument");
+  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] queries and pools must be 16-byte aligned");
+  const size_t need = pal_paged_attention_decode_workspace_size(
+      num_seqs, num_q_heads, head_dim, tokens_per_page, page_table_width, partition_size);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace of %zu bytes needed, %zu given",
+                need, workspace_bytes);
+  if (need > 0 && !aligned16(workspace))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 16-byte aligned");
+
+  pal::DecodeParams p;
+  p.q = static_cast<const uint16_t*>(queries);
+  p.k_pool = static_cast<const uint16_t*>(k_pool);
+  p.v_pool = static_cast<const uint16_t*>(v_pool);
+  p.page_table = page_table;
+  p.seq_lens = sequence_lengths;
+  p.out = static_cast<uint16_t*>(out);
+  const int64_t parts = page_table_width > 0 ? decode_max_parts(page_table_width, tokens_per_page, bpw) : 1;
+  p.max_parts = static_cast<int>(parts);
+  p.part_ml = static_cast<float*>(workspace);
+  p.part_o = need > 0 ? static_cast<float*>(workspace) + num_seqs * num_q_heads * parts * 2 : nullptr;
+  p.num_seqs = num_seqs;
+  p.num_pages = num_pages;
+  p.page_table_width = page_table_width;
+  p.num_q_heads = num_q_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_q_heads / num_kv_heads;
+  p.head_chunks = (p.group + 15) / 16;
+  p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
+  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, bpw, static_cast<hipStream_t>(stream)),
+                    "paged_attention_decode");
+}
+
+}  // extern "C"

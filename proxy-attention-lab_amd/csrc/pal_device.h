@@ -1,0 +1,111 @@
+// Device-side helpers shared by the gfx950 kernels: 16-bit float traits,
+// MFMA wrappers and wave64 reductions.
+//
+// Raw fp16/bf16 data is carried as 16-bit patterns inside 32-bit vector
+// registers (u32x2 / u32x4) and bit-cast to the operand types the MFMA
+// builtins want, so one kernel body serves both dtypes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pal_hip_internal.h"
+
+namespace pal {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// dtype traits: scalar conversion, packing and the MFMA shapes used here.
+//   mma16x16x32: A[16 x 32] * B[32 x 16] (8 elements per lane per operand)
+//   mma16x16x16: A[16 x 16] * B[16 x 16] (4 elements per lane per operand)
+//   mma32x32x16: A[32 x 16] * B[16 x 32] (8 elements per lane per operand)
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Dt;
+
+template <>
+struct Dt<kBF16> {
+  static __device__ __forceinline__ float to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(from_f32(lo)) | (static_cast<uint32_t>(from_f32(hi)) << 16);
+  }
+  static __device__ __forceinline__ f32x4 mma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Dt<kF16> {
+  static __device__ __forceinline__ float to_f32(uint16_t b) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, b));
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(from_f32(lo)) | (static_cast<uint32_t>(from_f32(hi)) << 16);
+  }
+  static __device__ __forceinline__ f32x4 mma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// wave64 helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// Index of this thread's wavefront, forced into a scalar register so that
+// addresses derived from it stay uniform (scalar loads of page-table entries).
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+}
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Zero the 16-bit elements i (0..3) of a packed 4-element vector whose
+// keep-bit is clear.
+__device__ __forceinline__ u32x2 mask4(u32x2 v, bool k0, bool k1, bool k2, bool k3) {
+  u32x2 r;
+  r.x = (k0 ? 0x0000FFFFu : 0u) | (k1 ? 0xFFFF0000u : 0u);
+  r.y = (k2 ? 0x0000FFFFu : 0u) | (k3 ? 0xFFFF0000u : 0u);
+  r.x &= v.x;
+  r.y &= v.y;
+  return r;
+}
+
+}  // namespace pal

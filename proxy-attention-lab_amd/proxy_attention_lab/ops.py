@@ -1,0 +1,228 @@
+"""Paged-attention operators over torch tensors on an MI355X (gfx950) device.
+
+Drop-in counterparts of the reference's ``proxy_attention_lab.ops``
+(src/proxy_attention_lab/ops.py:33-171): same function names, the same
+positional arguments in the same order and the same output shapes, with
+``torch.Tensor`` in place of ``mlx.core.array``.  Every operator runs on the
+HIP library libpal_hip.so through its C ABI; there is no CPU path.
+
+Differences from the reference, all deliberate:
+  * ``fill_kv_pages`` updates the pools in place and returns the same tensor
+    objects (the reference copies both whole pools on every call,
+    fill_kv_pages_primitive.cpp:91-92).  ``copy=True`` restores the
+    functional behaviour.
+  * ``stream`` takes ``None`` (current torch stream), a ``torch.cuda.Stream``
+    or a raw ``hipStream_t`` integer.
+  * ``paged_attention`` (fused mixed batch) is an addition; the reference has
+    no such function.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .layout import dtype_code, get_k_cache_stripe_size  # noqa: F401  (re-exported)
+
+__all__ = [
+    "fill_kv_pages",
+    "get_k_cache_stripe_size",
+    "paged_attention_decode",
+]
+
+
+# ---------------------------------------------------------------------------
+# argument plumbing
+# ---------------------------------------------------------------------------
+
+
+def _stream_handle(stream, device: torch.device) -> int:
+    if stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    if isinstance(stream, int):
+        return stream
+    raise TypeError(f"stream must be None, a torch.cuda.Stream or an int handle, got {type(stream)!r}")
+
+
+def _require_device(name: str, t: torch.Tensor, device: torch.device | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t)!r}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on a HIP device (got {t.device})")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _index_tensor(name: str, t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Return a contiguous 32-bit view/copy of an index tensor (u32/i32 bits)."""
+    _require_device(name, t, device)
+    if t.dtype in (torch.int32,):
+        return t.contiguous()
+    if t.dtype == torch.uint32:
+        return t.contiguous().view(torch.int32)
+    if t.dtype in (torch.int64, torch.int16, torch.uint8, torch.int8):
+        return t.to(torch.int32).contiguous()
+    raise ValueError(f"{name} must be an integer tensor, got {t.dtype}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    if nbytes <= 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# operators
+# ---------------------------------------------------------------------------
+
+
+def paged_attention_decode(
+    queries: torch.Tensor,
+    k_cache_pool: torch.Tensor,
+    v_cache_pool: torch.Tensor,
+    page_table: torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    stream=None,
+    *,
+    partition_size: int = 0,
+) -> torch.Tensor:
+    """Decode attention: one query row per sequence over its paged context.
+
+    Reference: ops.py:42-84 -> bindings.cpp:125-180 -> ops.cpp:36-108 ->
+    paged_attention_decode_primitive.cpp:71-266.
+
+    queries: [N, Hq, HD] (or [N, HD], meaning one query head); row s is the
+    query of sequence s and rows >= num_seqs are ignored.
+    k_cache_pool: [P, Hkv, HD/x, TPP, x]; v_cache_pool: [P, Hkv, HD, TPP].
+    page_table: [S, W] uint32/int32; sequence_lengths: [S] int32.
+    Returns [S, Hq, HD] in the query dtype (decode_primitive.cpp:289-300;
+    the "[N*Hq, HD]" in the reference docstring does not match its code).
+    ``partition_size`` (keyword-only, 0 = 512) sets the tokens per split-K
+    partition: 128, 256 or 512.
+    """
+    _require_device("queries", queries)
+    device = queries.device
+    for name, t in (("k_cache_pool", k_cache_pool), ("v_cache_pool", v_cache_pool)):
+        _require_device(name, t, device)
+    if v_cache_pool.dim() != 4:
+        raise ValueError("[paged_attention_decode] v_cache_pool must be 4D [pages, kv_heads, head_dim, tokens_per_page]")
+    if k_cache_pool.dim() != 5:
+        raise ValueError("[paged_attention_decode] k_cache_pool must be 5D [pages, kv_heads, head_dim/x, tokens_per_page, x]")
+    num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in v_cache_pool.shape)
+    if queries.dim() == 3:
+        num_rows, num_q_heads, q_hd = (int(x) for x in queries.shape)
+    elif queries.dim() == 2:
+        num_rows, q_hd = (int(x) for x in queries.shape)
+        num_q_heads = 1
+    else:
+        raise ValueError("[paged_attention_decode] queries must be 2D [N, HD] or 3D [N, Hq, HD]")
+    if q_hd != head_dim:
+        raise ValueError(f"[paged_attention_decode] query head_dim {q_hd} != cache head_dim {head_dim}")
+    code = dtype_code(queries.dtype)
+    if k_cache_pool.dtype != queries.dtype or v_cache_pool.dtype != queries.dtype:
+        raise ValueError("[paged_attention_decode] queries and pools must share one dtype")
+    expect_k = (num_pages, num_kv_heads, head_dim // 8, tpp, 8)
+    if tuple(k_cache_pool.shape) != expect_k:
+        raise ValueError(f"[paged_attention_decode] k_cache_pool shape {tuple(k_cache_pool.shape)} != {expect_k}")
+    if page_table.dim() != 2:
+        raise ValueError("[paged_attention_decode] page_table must be 2D [num_seqs, max_pages_per_seq]")
+    num_seqs, width = (int(x) for x in page_table.shape)
+    pt = _index_tensor("page_table", page_table, device)
+    lens = _index_tensor("sequence_lengths", sequence_lengths, device)
+    if lens.numel() < num_seqs:
+        raise ValueError(f"[paged_attention_decode] {lens.numel()} sequence lengths for {num_seqs} sequences")
+    q = queries.contiguous()
+    kp = k_cache_pool.contiguous()
+    vp = v_cache_pool.contiguous()
+    out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=queries.dtype, device=device)
+    L = _lib.lib()
+    ws_bytes = L.pal_paged_attention_decode_workspace_size(
+        num_seqs, num_q_heads, head_dim, tpp, width, int(partition_size)
+    )
+    ws = _workspace(ws_bytes, device)
+    status = L.pal_paged_attention_decode(
+        _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
+        code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
+        num_pages, width, int(partition_size),
+        _ptr(ws), ws_bytes, _stream_handle(stream, device),
+    )
+    _lib.check(status)
+    return out
+
+
+def fill_kv_pages(
+    new_keys: torch.Tensor,
+    new_values: torch.Tensor,
+    global_key_pool: torch.Tensor,
+    global_value_pool: torch.Tensor,
+    page_table: torch.Tensor,
+    current_token_write_positions: torch.Tensor,
+    query_to_seq_map: torch.Tensor,
+    stream=None,
+    *,
+    copy: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Scatter new K/V rows into their page slots (bit-exact copy).
+
+    Reference: ops.py:133-171 -> bindings.cpp:182-222 -> ops.cpp:188-239 ->
+    fill_kv_pages_primitive.cpp:70-170 -> fill_kv_pages.h.metal:56-116.
+
+    new_keys / new_values: [N, Hkv, HD]; pools as for decode;
+    current_token_write_positions: [N] int32; query_to_seq_map: [N] uint32.
+    Token t goes to page page_table[q2seq[t], pos // TPP], slot pos % TPP.
+    Updates the pools in place and returns them; with ``copy=True`` the
+    inputs are left untouched and fresh pools are returned, as in the
+    reference.
+    """
+    # ops.cpp:204-211: the same rank checks, first, raised as ValueError.
+    if global_key_pool.dim() != 5:
+        raise ValueError("[fill_kv_pages] global_key_pool must be 5D.")
+    if global_value_pool.dim() != 4:
+        raise ValueError("[fill_kv_pages] global_value_pool must be 4D.")
+    _require_device("new_keys", new_keys)
+    device = new_keys.device
+    for name, t in (("new_values", new_values), ("global_key_pool", global_key_pool),
+                    ("global_value_pool", global_value_pool)):
+        _require_device(name, t, device)
+    num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in global_value_pool.shape)
+    code = dtype_code(global_key_pool.dtype)
+    if not (new_keys.dtype == new_values.dtype == global_key_pool.dtype == global_value_pool.dtype):
+        raise ValueError("[fill_kv_pages] new keys/values and pools must share one dtype")
+    expect_k = (num_pages, num_kv_heads, head_dim // 8, tpp, 8)
+    if tuple(global_key_pool.shape) != expect_k:
+        raise ValueError(f"[fill_kv_pages] global_key_pool shape {tuple(global_key_pool.shape)} != {expect_k}")
+    if not global_key_pool.is_contiguous() or not global_value_pool.is_contiguous():
+        raise ValueError("[fill_kv_pages] pools must be contiguous (they are updated in place)")
+    n = int(new_keys.shape[0]) if new_keys.dim() > 0 else 0
+    if copy:
+        global_key_pool = global_key_pool.clone()
+        global_value_pool = global_value_pool.clone()
+    if n == 0 or new_keys.numel() == 0:
+        return global_key_pool, global_value_pool
+    if tuple(new_keys.shape) != (n, num_kv_heads, head_dim) or tuple(new_values.shape) != (n, num_kv_heads, head_dim):
+        raise ValueError(
+            f"[fill_kv_pages] new_keys/new_values must be [{n}, {num_kv_heads}, {head_dim}], got "
+            f"{tuple(new_keys.shape)} / {tuple(new_values.shape)}"
+        )
+    if page_table.dim() != 2:
+        raise ValueError("[fill_kv_pages] page_table must be 2D")
+    num_seqs, width = (int(x) for x in page_table.shape)
+    pt = _index_tensor("page_table", page_table, device)
+    pos = _index_tensor("current_token_write_positions", current_token_write_positions, device)
+    q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
+    if pos.numel() < n or q2s.numel() < n:
+        raise ValueError("[fill_kv_pages] write positions and query_to_seq_map need one entry per new token")
+    nk = new_keys.contiguous()
+    nv = new_values.contiguous()
+    status = _lib.lib().pal_fill_kv_pages(
+        _ptr(nk), _ptr(nv), _ptr(global_key_pool), _ptr(global_value_pool), _ptr(pt), _ptr(pos), _ptr(q2s),
+        code, n, num_kv_heads, head_dim, tpp, num_pages, num_seqs, width, _stream_handle(stream, device),
+    )
+    _lib.check(status)
+    return global_key_pool, global_value_pool
