@@ -85,8 +85,9 @@ class DecodeWorkload:
         pal.fill_kv_pages(self.new_k, self.new_v, self.k_pool, self.v_pool, self.page_table, self.write_pos,
                           self.q2seq)
 
-    def decode(self):
-        return pal.paged_attention_decode(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens)
+    def decode(self, partition_size: int = 0):
+        return pal.paged_attention_decode(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens,
+                                          partition_size=partition_size)
 
     # algorithmic bytes (each byte the operation must move at least once)
     def decode_bytes(self) -> int:
@@ -160,8 +161,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--rotate", type=int, default=4, help="independent workload copies cycled per step")
+    ap.add_argument("--partition", type=int, default=0, help="decode partition size (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before the timed loop, run one device-to-device copy of this many MiB (a kernel of "
+                         "known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -173,13 +178,21 @@ def main() -> int:
         return 1
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     works = [DecodeWorkload(seed=i) for i in range(max(1, args.rotate))]
     w0 = works[0]
     torch.cuda.synchronize()
 
     def step(w):
         w.fill()
-        return w.decode()
+        return w.decode(args.partition)
 
     for i in range(args.warmup):
         step(works[i % len(works)])
@@ -196,7 +209,7 @@ def main() -> int:
         w = works[i % len(works)]
         w.fill()
         dec_ev[i][0].record(stream)
-        w.decode()
+        w.decode(args.partition)
         dec_ev[i][1].record(stream)
     ev_end.record(stream)
     torch.cuda.synchronize()
@@ -228,6 +241,7 @@ def main() -> int:
                         "paged_attention_decode)",
             "num_seqs": w0.num_seqs, "ctx": "U[512,4096]", "num_q_heads": w0.hq, "num_kv_heads": w0.hkv,
             "head_dim": w0.hd, "tokens_per_page": w0.tpp, "rotated_copies": len(works),
+            "partition_size": args.partition or 512,
         },
         "tokens_per_s": round(w0.num_seqs / (ms_per_step * 1e-3), 1),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),

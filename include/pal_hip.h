@@ -83,14 +83,18 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
                       int64_t num_seqs, int64_t page_table_width, void* stream);
 
 /*
- * Workspace bytes needed by pal_paged_attention_decode for these shapes
- * (split-K partials: fp32 max / exp-sum and fp32 partial outputs).
- * partition_size: tokens per split (0 = library default, else 128, 256 or
- * 512; the reference's CHUNK_SIZE is 512, paged_attention_types.h:33).
+ * Workspace bytes pal_paged_attention_decode needs for these shapes on the
+ * current device (0 for unsupported arguments or when no device is present).
+ * The workspace holds the work plan and the fp32 partials (max, exp-sum,
+ * unnormalised output) of KV segments split between workers; its size
+ * follows from the number of workers the device keeps resident.
+ * partition_size: 0 (default: one equal share of the KV blocks per resident
+ * worker) or 128 / 256 / 512, a cap on the tokens one worker reduces (the
+ * reference's CHUNK_SIZE is 512, paged_attention_types.h:33).
  */
-size_t pal_paged_attention_decode_workspace_size(int64_t num_seqs, int num_q_heads, int head_dim,
-                                                 int tokens_per_page, int64_t page_table_width,
-                                                 int partition_size);
+size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, int num_q_heads,
+                                                 int num_kv_heads, int head_dim, int tokens_per_page,
+                                                 int64_t page_table_width, int partition_size);
 
 /*
  * Replaces paged_attention_decode (ops.py:42-84 -> bindings.cpp:125-180 ->
@@ -101,9 +105,12 @@ size_t pal_paged_attention_decode_workspace_size(int64_t num_seqs, int num_q_hea
  * Sequence s attends to tokens [0, sequence_lengths[s]) of its pages with
  * scale 1/sqrt(head_dim); query head h reads KV head
  * h / (num_q_heads / num_kv_heads).  A sequence of length <= 0 yields zeros.
- * Sequences longer than one partition are split across workgroups and
- * merged with a log-sum-exp pass (the reference's two-pass mode,
- * decode_primitive.cpp:100-102,163-240) using fp32 partials.
+ * The KV blocks of all sequences are split evenly over the device's
+ * resident workers; a sequence split between workers is merged with a
+ * log-sum-exp pass (the reference's two-pass mode,
+ * decode_primitive.cpp:100-102,163-240) from fp32 partials.  The workspace
+ * (256-byte aligned, size from pal_paged_attention_decode_workspace_size)
+ * must not be shared by concurrent calls.
  */
 int pal_paged_attention_decode(const void* queries, const void* k_pool, const void* v_pool,
                                const uint32_t* page_table, const int32_t* sequence_lengths,

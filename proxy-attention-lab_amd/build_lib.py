@@ -39,6 +39,9 @@ COMMON_FLAGS = [
 ]
 # Keep the compiler from selecting packed-FP32 (v_pk_*_f32) instructions.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Keep MFMA accumulators in ordinary VGPRs: the kernels rescale them with VALU
+# ops, and AGPR accumulators would cost a copy in and out around every rescale.
+DEVICE_FLAGS += ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def hipcc() -> str:

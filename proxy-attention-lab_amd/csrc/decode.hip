@@ -1,4 +1,5 @@
-// Split-K paged-attention decode for gfx950.
+// Paged-attention decode for gfx950: balanced ("stream-K") split of the KV
+// stream over a resident set of wavefront workers, then a log-sum-exp merge.
 //
 // Reference behaviour: kernels/paged_attention/decode/paged_attention_decode.h.metal
 // (one query row per sequence, GQA map h -> h / (Hq/Hkv) at :64-65, scale
@@ -6,313 +7,597 @@
 // merge of decode/paged_reduce_decode.h.metal:79-128.
 //
 // Design (MI355X):
-//  * One workgroup = 4 wavefronts = one (partition, kv head, head chunk,
-//    sequence).  All query heads that share the kv head (up to 16 per chunk)
-//    are processed together, so every K/V page block is read from HBM once per
-//    GQA group instead of once per query head.
-//  * The unit of work is a 16-token block (one page for TPP=16, half a page
-//    for TPP=32).  Wave w of the workgroup takes blocks w, w+4, w+8, ... of the
-//    partition.
-//  * QK^T runs on MFMA as S^T = K * Q^T with v_mfma_f32_16x16x32: the A operand
-//    is the K page block exactly as it lies in the striped pool layout
-//    [HD/8][TPP][8] -- lane l loads the 16-byte stripe (l/16 + 4kk) of token
-//    l%16, so 64 lanes read 1 KiB contiguous per instruction.  The result
-//    leaves head l%16 and tokens 4(l/16)..+3 in lane l, which is exactly the A
-//    operand layout of v_mfma_f32_16x16x16 for P*V, so probabilities never
-//    cross lanes.  V is read as 8-byte runs of 4 tokens from the [HD][TPP]
-//    layout.
-//  * Softmax: scores of all blocks of the partition stay in registers; the
-//    workgroup max is exchanged once through LDS, so there is no running
-//    rescale.  Each partition writes either the final output (single
-//    partition) or fp32 partials (max, exp-sum, unnormalised O) that the merge
-//    kernel combines with a log-sum-exp reduction.
+//  * Work is the flat list of (sequence, kv head, head chunk) "segments", each
+//    a run of 16-token blocks (one page for TPP=16, half a page for TPP=32).
+//    All query heads sharing a kv head (up to 16 per chunk) are processed
+//    together, so a K/V page block is read from HBM once per GQA group.
+//  * The sequence lengths are scanned (by every worker itself for batches of
+//    up to 1024 sequences, else by decode_plan_kernel) and every worker (one
+//    wavefront) gets an equal share of the total blocks: worker w owns global
+//    blocks [w*T/NW, (w+1)*T/NW).  Every worker therefore streams
+//    the same number of bytes and the grid drains evenly -- no tail of
+//    half-empty partitions.  NW is sized to what the GPU keeps resident.
+//  * A worker streams its blocks with a software pipeline: the K and V loads
+//    of the next PF blocks are in flight while the current block is computed.
+//    The K block is read in the pool's striped [HD/8][TPP][8] layout, which is
+//    exactly the A operand of v_mfma_f32_16x16x32 for S^T = K * Q^T (lane l
+//    loads the 16-byte stripe (l/16 + 4kk) of token l%16: 1 KiB contiguous
+//    per instruction).  The result holds head l%16 and tokens 4(l/16)..+3 in
+//    lane l, which is the B operand of v_mfma_f32_16x16x16 for
+//    O^T = V^T * P^T; V is read as 8-byte runs of 4 tokens from the [HD][TPP]
+//    layout as its A operand.  In O^T the head is the lane, so the online
+//    softmax rescale is a per-lane multiply.
+//  * A segment that lies wholly inside one worker writes the normalised output
+//    directly.  Segments split across workers leave fp32 partials
+//    (max, exp-sum, unnormalised O) in one of two slots per worker, combined
+//    by decode_merge_kernel.
 #include "pal_device.h"
+
+#ifndef PAL_DECODE_PREFETCH
+#define PAL_DECODE_PREFETCH 2  // blocks whose loads are in flight ahead of the one being computed
+#endif
 
 namespace pal {
 
 namespace {
 
-constexpr int kNW = 4;  // wavefronts per workgroup
+constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
+constexpr int kPlanThreads = 1024;
+constexpr int kInlinePlanSeqs = 1024;  // largest batch planned inside the stream kernel
 
-template <int DT, int HD, int TPP, int BPW>
-__global__ __launch_bounds__(kNW * kWave) void decode_partition_kernel(const DecodeParams p) {
+__device__ __forceinline__ int64_t seq_blocks(const DecodeParams& p, int64_t s, int tpp) {
+  const int64_t max_tokens = p.page_table_width * tpp;
+  int64_t len = p.seq_lens[s];
+  len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
+  return (len + 15) >> 4;
+}
+
+__device__ __forceinline__ int64_t worker_start(int64_t w, int64_t total, int64_t nw) { return (w * total) / nw; }
+
+// Worker that owns global block b (total > 0).
+__device__ __forceinline__ int64_t worker_of(int64_t b, int64_t total, int64_t nw) {
+  return ((b + 1) * nw + total - 1) / total - 1;
+}
+
+// Block-wide inclusive scan of int64 values (blockDim.x == kPlanThreads).
+__device__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_sums) {
+  const int lane = lane_id();
+  const int wv = static_cast<int>(threadIdx.x) >> 6;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t o = __shfl_up(v, off, kWave);
+    if (lane >= off) v += o;
+  }
+  if (lane == kWave - 1) wave_sums[wv] = v;
+  __syncthreads();
+  int64_t add = 0;
+  for (int i = 0; i < wv; ++i) add += wave_sums[i];
+  __syncthreads();
+  return v + add;
+}
+
+// Scans the sequence lengths: cum[s] = first global block of sequence s (all
+// of its segments), hdr = {T, NW_eff}, plan[w] = {sequence, block offset in
+// that sequence's segments} of worker w's first block.
+template <int TPP>
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeParams p) {
+  __shared__ int64_t wave_sums[kPlanThreads / kWave];
+  __shared__ int64_t total_sh;
+  const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
+  const int tid = threadIdx.x;
+
+  int64_t local = 0;
+  for (int64_t s = tid; s < p.num_seqs; s += kPlanThreads) local += seq_blocks(p, s, TPP) * segs;
+  const int64_t incl = block_inclusive_scan(local, wave_sums);
+  if (tid == kPlanThreads - 1) total_sh = incl;
+  __syncthreads();
+  const int64_t total = total_sh;
+  int64_t nw = p.num_workers;
+  if (p.tokens_per_worker > 0) {
+    int64_t want = (total * 16 + p.tokens_per_worker - 1) / p.tokens_per_worker;
+    if (want < p.min_workers) want = p.min_workers;
+    if (want < nw) nw = want;
+  }
+  if (nw > total) nw = total > 0 ? total : 1;
+  if (tid == 0) {
+    p.hdr[0] = total;
+    p.hdr[1] = nw;
+  }
+
+  int64_t carry = 0;
+  for (int64_t base = 0; base < p.num_seqs; base += kPlanThreads) {
+    const int64_t s = base + tid;
+    const int64_t v = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
+    const int64_t inc = block_inclusive_scan(v, wave_sums);
+    const int64_t start = carry + inc - v;
+    if (s < p.num_seqs) {
+      p.cum[s] = start;
+      if (v > 0) {
+        // workers whose first block falls in [start, start + v)
+        const int64_t wa = (start * nw + total - 1) / total;
+        const int64_t wb = ((start + v) * nw + total - 1) / total;
+        for (int64_t w = wa; w < wb; ++w) {
+          p.plan[2 * w + 0] = s;
+          p.plan[2 * w + 1] = worker_start(w, total, nw) - start;
+        }
+      }
+    }
+    if (tid == kPlanThreads - 1) total_sh = inc;
+    __syncthreads();
+    carry += total_sh;
+    __syncthreads();
+  }
+  if (tid == 0) p.cum[p.num_seqs] = total;
+}
+
+// Plan computed by one wavefront from the sequence lengths (S <= kInlinePlanSeqs):
+// lane l sums the blocks of sequences [16 l, 16 l + 16), a wave scan gives
+// every lane's first global block, and the lane whose range holds block b0
+// walks its sequences to find the one containing it.  The worker with id 0
+// also stores hdr and cum[] for the merge kernel.
+struct WavePlan {
+  int64_t total;  // T
+  int64_t nw;     // workers in use
+  int64_t s;      // sequence of the worker's first block
+  int64_t r;      // its block offset within that sequence's segments
+};
+
+template <int TPP>
+__device__ WavePlan wave_plan(const DecodeParams& p, int64_t w) {
+  constexpr int K = kInlinePlanSeqs / kWave;
+  const int lane = lane_id();
+  const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
+  int64_t nb[K];
+  int64_t lane_sum = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int64_t s = static_cast<int64_t>(lane) * K + k;
+    nb[k] = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
+    lane_sum += nb[k];
+  }
+  int64_t incl = lane_sum;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t o = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += o;
+  }
+  const int64_t excl = incl - lane_sum;
+  WavePlan wp;
+  wp.total = __shfl(incl, kWave - 1, kWave);
+  int64_t nw = p.num_workers;
+  if (p.tokens_per_worker > 0) {
+    int64_t want = (wp.total * 16 + p.tokens_per_worker - 1) / p.tokens_per_worker;
+    if (want < p.min_workers) want = p.min_workers;
+    if (want < nw) nw = want;
+  }
+  if (nw > wp.total) nw = wp.total > 0 ? wp.total : 1;
+  wp.nw = nw;
+  if (w == 0) {
+    int64_t c = excl;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t s = static_cast<int64_t>(lane) * K + k;
+      if (s < p.num_seqs) p.cum[s] = c;
+      c += nb[k];
+    }
+    if (lane == 0) {
+      p.hdr[0] = wp.total;
+      p.hdr[1] = nw;
+      p.cum[p.num_seqs] = wp.total;
+    }
+  }
+  wp.s = 0;
+  wp.r = 0;
+  if (wp.total == 0 || w >= nw) return wp;
+  const int64_t b0 = worker_start(w, wp.total, nw);
+  const uint64_t owner = __ballot(lane_sum > 0 && excl <= b0 && b0 < incl);
+  const int L = __builtin_ctzll(owner);
+  int64_t s_found = 0, r_found = 0;
+  int64_t c = excl;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (s_found == 0 && r_found == 0 && b0 >= c && b0 < c + nb[k]) {
+      s_found = static_cast<int64_t>(lane) * K + k + 1;  // +1: 0 means "not found yet"
+      r_found = b0 - c;
+    }
+    c += nb[k];
+  }
+  wp.s = __shfl(s_found, L, kWave) - 1;
+  wp.r = __shfl(r_found, L, kWave);
+  return wp;
+}
+
+template <int DT, int HD, int TPP>
+__global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel(const DecodeParams p) {
   constexpr bool kK32 = (HD % 32) == 0;  // QK k-step of 32 (else 16)
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
-  constexpr int NT = HD / 16;            // PV output tiles of 16 dims
-  extern __shared__ float smem[];        // [kNW][hg][HD] partial outputs
-  __shared__ float red_m[kNW][16];
-  __shared__ float red_l[kNW][16];
+  constexpr int NT = HD / 16;            // output tiles of 16 dims
+  constexpr int PF = PAL_DECODE_PREFETCH;
+  constexpr int NBUF = PF + 1;
+  // Blocks whose page ids one vector load (one id per lane) always covers,
+  // whatever the alignment of the first block within its page.
+  constexpr int kChunkBlocks = (kWave - 1) * TPP / 16;
 
-  const int part = blockIdx.x;
-  const int kvh = blockIdx.y / p.head_chunks;
-  const int h0 = (blockIdx.y % p.head_chunks) * 16;
-  const int hg = min(16, p.group - h0);
-  const int64_t s = blockIdx.z;
-  const int qh_base = kvh * p.group + h0;
-  const int64_t max_tokens = p.page_table_width * TPP;
-  const int len = static_cast<int>(min<int64_t>(max<int32_t>(p.seq_lens[s], 0), max_tokens));
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
+  int64_t total, nw, s, r;
+  if (p.num_seqs <= kInlinePlanSeqs) {
+    const WavePlan wp = wave_plan<TPP>(p, w);
+    total = wp.total;
+    nw = wp.nw;
+    s = wp.s;
+    r = wp.r;
+  } else {  // planned by decode_plan_kernel
+    total = p.hdr[0];
+    nw = p.hdr[1];
+    if (w >= nw || total == 0) return;
+    s = p.plan[2 * w + 0];
+    r = p.plan[2 * w + 1];
+  }
+  if (w >= nw || total == 0) return;
+  const int64_t b0 = worker_start(w, total, nw);
+  int64_t remaining = worker_start(w + 1, total, nw) - b0;
+  if (remaining <= 0) return;
 
   const int lane = lane_id();
   const int g = lane >> 4;
   const int r16 = lane & 15;
-  const int w = wave_id();
-
-  const int blocks_seq = (len + 15) >> 4;
-  constexpr int kBlocksPart = kNW * BPW;
-  const int nparts = (blocks_seq + kBlocksPart - 1) / kBlocksPart;
-
-  if (len == 0) {
-    if (part == 0) {
-      for (int idx = threadIdx.x; idx < hg * HD; idx += kNW * kWave) {
-        p.out[(s * p.num_q_heads + qh_base + idx / HD) * HD + idx % HD] = 0;
-      }
-    }
-    return;
-  }
-  if (part >= nparts) return;
-
-  // Q^T operand: lane holds Q[head r16][k-slice of this lane] for every k-step.
-  u32x4 qv4[kK32 ? KK : 1];
-  u32x2 qv2[kK32 ? 1 : KK];
-  {
-    const bool hv = r16 < hg;
-    const uint16_t* qrow = p.q + (s * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if constexpr (kK32) {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        qv4[kk] = hv ? *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * g) : z;
-      } else {
-        const u32x2 z = {0u, 0u};
-        qv2[kk] = hv ? *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 4 * g) : z;
-      }
-    }
-  }
-
+  const int segs = p.num_kv_heads * p.head_chunks;
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;  // elements per (page, kv head)
   const int64_t page_stride = head_block * p.num_kv_heads;
-  const uint16_t* kbase = p.k_pool + kvh * head_block;
-  const uint16_t* vbase = p.v_pool + kvh * head_block;
-  const uint32_t* pt = p.page_table + s * p.page_table_width;
-  const int b_first = part * kBlocksPart;
+  const int64_t max_tokens = p.page_table_width * TPP;
+  bool first = true;
 
-  // ---- S^T = K * Q^T for every block of this wave -------------------------
-  f32x4 sc[BPW];
-  float mloc = -INFINITY;
+  while (remaining > 0) {
+    int64_t len = p.seq_lens[s];
+    len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
+    const int64_t nb = (len + 15) >> 4;
+    if (nb == 0) {  // empty sequence: no blocks, move on
+      ++s;
+      r = 0;
+      continue;
+    }
+    const int seg = static_cast<int>(r / nb);
+    const int64_t blk = r - seg * nb;
+    const int64_t count = (nb - blk) < remaining ? (nb - blk) : remaining;
+    const int kvh = seg / p.head_chunks;
+    const int h0 = (seg % p.head_chunks) * 16;
+    const int hg = min(16, p.group - h0);
+    const int qh_base = kvh * p.group + h0;
+    const bool complete = (blk == 0) && (count == nb);
+
+    // Q^T operand: lane holds Q[head r16][k-slice of this lane] (padding heads zeroed).
+    u32x4 qv4[kK32 ? KK : 1];
+    u32x2 qv2[kK32 ? 1 : KK];
+    {
+      const bool hv = r16 < hg;
+      const uint32_t qmask = hv ? 0xFFFFFFFFu : 0u;
+      const uint16_t* qrow = p.q + (s * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
 #pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-    const int b = b_first + j * kNW + w;
-    const float ninf = -INFINITY;
-    sc[j] = f32x4{ninf, ninf, ninf, ninf};
-    if (b < blocks_seq) {
-      const uint32_t page = pt[(b * 16) / TPP];
-      if (page < p.num_pages) {
-        const int slot0 = (b * 16) % TPP;
+      for (int kk = 0; kk < KK; ++kk) {
+        if constexpr (kK32) {
+          qv4[kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * g) & qmask;
+        } else {
+          qv2[kk] = *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 4 * g) & qmask;
+        }
+      }
+    }
+
+    const uint16_t* kbase = p.k_pool + kvh * head_block;
+    const uint16_t* vbase = p.v_pool + kvh * head_block;
+    const uint32_t* pt = p.page_table + s * p.page_table_width;
+
+    float m_run = -INFINITY;  // running max (raw score units) of head r16
+    float l_run = 0.f;        // this lane's share of the exp-sum of head r16
+    f32x4 o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t c0 = 0; c0 < count; c0 += kChunkBlocks) {
+      const int n_blk = static_cast<int>((count - c0) < kChunkBlocks ? (count - c0) : kChunkBlocks);
+      const int64_t bstart = blk + c0;            // first block of this chunk
+      const int64_t pbase = (bstart * 16) / TPP;  // its page index
+      int64_t lp = pbase + lane;
+      if (lp >= p.page_table_width) lp = p.page_table_width - 1;
+      const uint32_t pid = pt[lp];
+
+      u32x4 kb4[NBUF][kK32 ? KK : 1];
+      u32x2 kb2[NBUF][kK32 ? 1 : KK];
+      u32x2 vb[NBUF][NT];
+      bool bv[NBUF];
+
+      // Issue the K and V loads of chunk block i into buffer `buf`.  An
+      // out-of-range page id is replaced by page 0 (in bounds) and the block
+      // is masked out when computed.
+      auto issue = [&](int i, int buf) {
+        const int64_t b = bstart + i;
+        const uint32_t pg = __builtin_amdgcn_readlane(pid, static_cast<int>((b * 16) / TPP - pbase));
+        bv[buf] = pg < p.num_pages;
+        const uint32_t page = bv[buf] ? pg : 0u;
+        const int slot0 = static_cast<int>((b * 16) % TPP);
         const uint16_t* kp = kbase + static_cast<int64_t>(page) * page_stride;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const uint16_t* vp = vbase + static_cast<int64_t>(page) * page_stride + slot0 + 4 * g;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
           if constexpr (kK32) {
             const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
-            const u32x4 kv = *reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8);
-            acc = Dt<DT>::mma16x16x32(kv, qv4[kk], acc);
+            kb4[buf][kk] = *reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8);
           } else {
             const int d = 16 * kk + 4 * g;  // dims d .. d+3
-            const u32x2 kv = *reinterpret_cast<const u32x2*>(
-                kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7));
-            acc = Dt<DT>::mma16x16x16(kv, qv2[kk], acc);
+            kb2[buf][kk] = *reinterpret_cast<const u32x2*>(kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7));
           }
         }
-        const int t0 = b * 16 + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[j][i] = (t0 + i < len) ? acc[i] : ninf;
-          mloc = fmaxf(mloc, sc[j][i]);
-        }
-      }
-    }
-  }
+        for (int n = 0; n < NT; ++n) vb[buf][n] = *reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP);
+      };
 
-  // ---- workgroup max per head ---------------------------------------------
-  mloc = fmaxf(mloc, shfl_xor(mloc, 16));
-  mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-  if (g == 0) red_m[w][r16] = mloc;
-  __syncthreads();
-  float m = red_m[0][r16];
+      auto compute = [&](int i, int buf) {
+        const int64_t b = bstart + i;
+        const bool live = bv[buf] && i < n_blk;  // steps past the chunk end are fully masked
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ww = 1; ww < kNW; ++ww) m = fmaxf(m, red_m[ww][r16]);
-  // A head whose every score is masked (all pages invalid) keeps m = -inf;
-  // use 0 so that exp2 yields 0 instead of NaN.
-  const float msc = (m == -INFINITY) ? 0.f : m * p.scale_log2;
-
-  // ---- P = exp(S - m), O += P * V -----------------------------------------
-  float lsum = 0.f;
-  f32x4 o[NT];
-#pragma unroll
-  for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < BPW; ++j) {
-    const int b = b_first + j * kNW + w;
-    if (b < blocks_seq) {
-      const uint32_t page = pt[(b * 16) / TPP];
-      if (page < p.num_pages) {
-        float e[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          e[i] = __builtin_amdgcn_exp2f(fmaf(sc[j][i], p.scale_log2, -msc));
-          lsum += e[i];
+        for (int kk = 0; kk < KK; ++kk) {
+          if constexpr (kK32) {
+            acc = Dt<DT>::mma16x16x32(kb4[buf][kk], qv4[kk], acc);
+          } else {
+            acc = Dt<DT>::mma16x16x16(kb2[buf][kk], qv2[kk], acc);
+          }
         }
-        const u32x2 pa = {Dt<DT>::pack2(e[0], e[1]), Dt<DT>::pack2(e[2], e[3])};
-        const int slot0 = (b * 16) % TPP;
-        const uint16_t* vp = vbase + static_cast<int64_t>(page) * page_stride + slot0 + 4 * g;
-        const int t0 = b * 16 + 4 * g;
-        const bool tail = (b * 16 + 16) > len;
+        // tokens past the end (and whole invalid blocks) are masked
+        const int64_t t0 = live ? b * 16 + 4 * g : len;
+        float sc[4];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sc[e] = (t0 + e < len) ? acc[e] : -INFINITY;
+          bm = fmaxf(bm, sc[e]);
+        }
+        bm = fmaxf(bm, shfl_xor(bm, 16));
+        bm = fmaxf(bm, shfl_xor(bm, 32));
+        const float m_new = fmaxf(m_run, bm);
+        const float msc = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
+        if (__ballot(m_new > m_run && m_run != -INFINITY)) {
+          // the max of some head grew: rescale the running state
+          const float alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(fmaf(m_run, p.scale_log2, -msc));
+          l_run *= alpha;
+#pragma unroll
+          for (int n = 0; n < NT; ++n) o[n] *= alpha;
+        }
+        m_run = m_new;
+        float pe[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pe[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], p.scale_log2, -msc));
+          l_run += pe[e];
+        }
+        const u32x2 pb = {Dt<DT>::pack2(pe[0], pe[1]), Dt<DT>::pack2(pe[2], pe[3])};
+        // slots past the end may hold anything, NaN bits included: zero their
+        // V (branch-free: two ANDs per tile)
+        const uint32_t mlo = (t0 < len ? 0x0000FFFFu : 0u) | (t0 + 1 < len ? 0xFFFF0000u : 0u);
+        const uint32_t mhi = (t0 + 2 < len ? 0x0000FFFFu : 0u) | (t0 + 3 < len ? 0xFFFF0000u : 0u);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          u32x2 vv = *reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP);
-          // Slots past the sequence end may hold anything (NaN bits included):
-          // zero them so that 0 * garbage cannot poison the sum.
-          if (tail) vv = mask4(vv, t0 < len, t0 + 1 < len, t0 + 2 < len, t0 + 3 < len);
-          o[n] = Dt<DT>::mma16x16x16(pa, vv, o[n]);
+          const u32x2 vv = {vb[buf][n].x & mlo, vb[buf][n].y & mhi};
+          o[n] = Dt<DT>::mma16x16x16(vv, pb, o[n]);
+        }
+      };
+
+      // Every step issues and computes unconditionally (steps past the end
+      // re-read the last block, an L2 hit, and compute it fully masked): with
+      // no load under a branch the compiler's wait counts stay exact, so the
+      // PF blocks in flight are never drained early.
+#pragma unroll
+      for (int q = 0; q < PF; ++q) issue(q < n_blk ? q : n_blk - 1, q);
+      for (int i0 = 0; i0 < n_blk; i0 += NBUF) {
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) {
+          const int i = i0 + u;
+          issue(i + PF < n_blk ? i + PF : n_blk - 1, (u + PF) % NBUF);
+          compute(i, u);
         }
       }
     }
-  }
 
-  // ---- combine the 4 waves --------------------------------------------------
-  lsum += shfl_xor(lsum, 16);
-  lsum += shfl_xor(lsum, 32);
-  if (g == 0) red_l[w][r16] = lsum;
+    // ---- finish the segment: exp-sum of head r16 across the 4 lane groups --
+    float l = l_run;
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    if (r16 < hg) {
+      const int64_t row = s * p.num_q_heads + qh_base + r16;
+      if (complete) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {
+        for (int n = 0; n < NT; ++n) {
+          const u32x2 pk = {Dt<DT>::pack2(o[n][0] * inv, o[n][1] * inv), Dt<DT>::pack2(o[n][2] * inv, o[n][3] * inv)};
+          *reinterpret_cast<u32x2*>(p.out + row * HD + 16 * n + 4 * g) = pk;
+        }
+      } else {
+        const int64_t slot = (w * 2 + (first ? 0 : 1)) * p.hg_max + r16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * g + i;
-      if (h < hg) smem[(w * hg + h) * HD + 16 * n + r16] = o[n][i];
-    }
-  }
-  __syncthreads();
-
-  for (int idx = threadIdx.x; idx < hg * HD; idx += kNW * kWave) {
-    const int h = idx / HD;
-    const int d = idx - h * HD;
-    float acc = smem[h * HD + d];
-    float l = red_l[0][h];
-    float mh = red_m[0][h];
-#pragma unroll
-    for (int ww = 1; ww < kNW; ++ww) {
-      acc += smem[(ww * hg + h) * HD + d];
-      l += red_l[ww][h];
-      mh = fmaxf(mh, red_m[ww][h]);
-    }
-    const int64_t row = s * p.num_q_heads + qh_base + h;
-    if (nparts == 1) {
-      p.out[row * HD + d] = Dt<DT>::from_f32(l > 0.f ? acc / l : 0.f);
-    } else {
-      const int64_t slot = row * p.max_parts + part;
-      p.part_o[slot * HD + d] = acc;
-      if (d == 0) {
-        p.part_ml[slot * 2 + 0] = (mh == -INFINITY) ? -INFINITY : mh * p.scale_log2;
-        p.part_ml[slot * 2 + 1] = l;
+        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(p.part_o + slot * HD + 16 * n + 4 * g) = o[n];
+        if (g == 0) {
+          p.part_ml[slot * 2 + 0] = (m_run == -INFINITY) ? -INFINITY : m_run * p.scale_log2;
+          p.part_ml[slot * 2 + 1] = l;
+        }
       }
     }
+
+    remaining -= count;
+    r += count;
+    if (r >= nb * segs) {
+      ++s;
+      r = 0;
+    }
+    first = false;
   }
 }
 
-// Log-sum-exp merge of the partitions of one (sequence, query head) per
-// wavefront: M = max_c m_c, out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
-template <int DT, int HD, int TPP, int BPW>
-__global__ __launch_bounds__(kNW * kWave) void decode_merge_kernel(const DecodeParams p) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kNW + wave_id();
+// One wavefront per (sequence, query head): combines the partials of a
+// segment that several workers shared, M = max_c m_c,
+// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  Lane j fetches the
+// (m, l) of the j-th contributing worker so those loads go out together; the
+// O loads of consecutive workers are unrolled to keep several in flight.
+// Empty sequences get zeros; segments finished by one worker are already out.
+template <int DT, int HD, int TPP>
+__global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_merge_kernel(const DecodeParams p) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
   if (row >= p.num_seqs * p.num_q_heads) return;
   const int64_t s = row / p.num_q_heads;
-  const int64_t max_tokens = p.page_table_width * TPP;
-  const int len = static_cast<int>(min<int64_t>(max<int32_t>(p.seq_lens[s], 0), max_tokens));
-  constexpr int kBlocksPart = kNW * BPW;
-  const int nparts = (((len + 15) >> 4) + kBlocksPart - 1) / kBlocksPart;
-  if (nparts <= 1) return;
-  const float* ml = p.part_ml + row * p.max_parts * 2;
-  float big_m = -INFINITY;
-  for (int c = 0; c < nparts; ++c) big_m = fmaxf(big_m, ml[2 * c]);
-  if (big_m == -INFINITY) big_m = 0.f;
-  float big_l = 0.f;
-  for (int c = 0; c < nparts; ++c) big_l += ml[2 * c + 1] * __builtin_amdgcn_exp2f(ml[2 * c] - big_m);
-  const float inv_l = big_l > 0.f ? 1.f / big_l : 0.f;
-  const float* po = p.part_o + row * p.max_parts * HD;
+  const int qh = static_cast<int>(row - s * p.num_q_heads);
   const int lane = lane_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
-  float acc[kPer];
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
-  for (int c = 0; c < nparts; ++c) {
-    const float wgt = __builtin_amdgcn_exp2f(ml[2 * c] - big_m);
+  const int64_t nb = seq_blocks(p, s, TPP);
+  const int64_t total = p.hdr[0];
+  const int64_t nw = p.hdr[1];
+  const int64_t cum_s = p.cum[s];
+  if (nb == 0) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int d = lane + e * kWave;
-      if (d < HD) acc[e] += wgt * po[c * HD + d];
+      if (d < HD) p.out[row * HD + d] = 0;
+    }
+    return;
+  }
+  const int kvh = qh / p.group;
+  const int hl = qh - kvh * p.group;
+  const int seg = kvh * p.head_chunks + hl / 16;
+  const int h = hl % 16;
+  const int64_t g0 = cum_s + seg * nb;
+  const int64_t g1 = g0 + nb;
+  const int64_t w0 = worker_of(g0, total, nw);
+  const int64_t w1 = worker_of(g1 - 1, total, nw);
+  if (w0 == w1) return;
+  const int64_t n = w1 - w0 + 1;
+
+  auto slot_of = [&](int64_t w) { return (w * 2 + (worker_start(w, total, nw) >= g0 ? 0 : 1)) * p.hg_max + h; };
+
+  float big_m = -INFINITY;
+  for (int64_t base = 0; base < n; base += kWave) {
+    const int64_t j = base + lane;
+    const float m = j < n ? p.part_ml[slot_of(w0 + j) * 2] : -INFINITY;
+    big_m = fmaxf(big_m, m);
+  }
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) big_m = fmaxf(big_m, shfl_xor(big_m, off));
+  const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
+
+  float lsum = 0.f;
+  float acc[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
+  for (int64_t base = 0; base < n; base += kWave) {
+    const int64_t j = base + lane;
+    float wgt = 0.f;
+    if (j < n) {
+      const int64_t sl = slot_of(w0 + j);
+      wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
+      lsum += wgt * p.part_ml[sl * 2 + 1];
+    }
+    const int cnt = static_cast<int>((n - base) < kWave ? (n - base) : kWave);
+#pragma unroll 8
+    for (int jj = 0; jj < cnt; ++jj) {
+      const float wj = __shfl(wgt, jj, kWave);
+      const float* po = p.part_o + slot_of(w0 + base + jj) * HD;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int d = lane + e * kWave;
+        if (d < HD) acc[e] += wj * po[d];
+      }
     }
   }
 #pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) lsum += shfl_xor(lsum, off);
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
   for (int e = 0; e < kPer; ++e) {
     const int d = lane + e * kWave;
-    if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[e] * inv_l);
+    if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[e] * inv);
   }
-}
-
-template <int DT, int HD, int TPP, int BPW>
-hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
-  const int hg_max = p.group < 16 ? p.group : 16;
-  const size_t smem = static_cast<size_t>(kNW) * hg_max * HD * sizeof(float);
-  const dim3 grid(p.max_parts, p.num_kv_heads * p.head_chunks, static_cast<unsigned>(p.num_seqs));
-  hipLaunchKernelGGL((decode_partition_kernel<DT, HD, TPP, BPW>), grid, dim3(kNW * kWave), smem,
-                     stream, p);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || p.max_parts <= 1) return err;
-  const int64_t rows = p.num_seqs * p.num_q_heads;
-  const dim3 mgrid(static_cast<unsigned>((rows + kNW - 1) / kNW));
-  hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP, BPW>), mgrid, dim3(kNW * kWave), 0, stream,
-                     p);
-  return hipGetLastError();
 }
 
 template <int DT, int HD, int TPP>
-hipError_t dispatch_bpw(const DecodeParams& p, int bpw, hipStream_t stream) {
-  switch (bpw) {
-    case 2: return launch_decode_t<DT, HD, TPP, 2>(p, stream);
-    case 4: return launch_decode_t<DT, HD, TPP, 4>(p, stream);
-    case 8: return launch_decode_t<DT, HD, TPP, 8>(p, stream);
-    default: return hipErrorInvalidValue;
+hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+  hipError_t err;
+  if (p.num_seqs > kInlinePlanSeqs) {
+    hipLaunchKernelGGL((decode_plan_kernel<TPP>), dim3(1), dim3(kPlanThreads), 0, stream, p);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
   }
+  const int64_t groups = (static_cast<int64_t>(p.num_workers) + kWorkersPerGroup - 1) / kWorkersPerGroup;
+  hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)),
+                     dim3(kWorkersPerGroup * kWave), 0, stream, p);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int64_t rows = p.num_seqs * p.num_q_heads;
+  hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>),
+                     dim3(static_cast<unsigned>((rows + kWorkersPerGroup - 1) / kWorkersPerGroup)),
+                     dim3(kWorkersPerGroup * kWave), 0, stream, p);
+  return hipGetLastError();
 }
 
 template <int DT, int HD>
-hipError_t dispatch_tpp(const DecodeParams& p, int tpp, int bpw, hipStream_t stream) {
+hipError_t dispatch_tpp(const DecodeParams& p, int tpp, hipStream_t stream) {
   switch (tpp) {
-    case 16: return dispatch_bpw<DT, HD, 16>(p, bpw, stream);
-    case 32: return dispatch_bpw<DT, HD, 32>(p, bpw, stream);
+    case 16: return launch_decode_t<DT, HD, 16>(p, stream);
+    case 32: return launch_decode_t<DT, HD, 32>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int DT>
-hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, int bpw, hipStream_t stream) {
+hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, hipStream_t stream) {
   switch (hd) {
-    case 32: return dispatch_tpp<DT, 32>(p, tpp, bpw, stream);
-    case 64: return dispatch_tpp<DT, 64>(p, tpp, bpw, stream);
-    case 80: return dispatch_tpp<DT, 80>(p, tpp, bpw, stream);
-    case 96: return dispatch_tpp<DT, 96>(p, tpp, bpw, stream);
-    case 128: return dispatch_tpp<DT, 128>(p, tpp, bpw, stream);
-    case 256: return dispatch_tpp<DT, 256>(p, tpp, bpw, stream);
+    case 32: return dispatch_tpp<DT, 32>(p, tpp, stream);
+    case 64: return dispatch_tpp<DT, 64>(p, tpp, stream);
+    case 80: return dispatch_tpp<DT, 80>(p, tpp, stream);
+    case 96: return dispatch_tpp<DT, 96>(p, tpp, stream);
+    case 128: return dispatch_tpp<DT, 128>(p, tpp, stream);
+    case 256: return dispatch_tpp<DT, 256>(p, tpp, stream);
     default: return hipErrorInvalidValue;
+  }
+}
+
+template <int DT, int HD, int TPP>
+const void* stream_kernel_ptr() {
+  return reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP>);
+}
+
+template <int DT>
+const void* stream_kernel_for(int hd, int tpp) {
+  const bool t32 = tpp == 32;
+  switch (hd) {
+    case 32: return t32 ? stream_kernel_ptr<DT, 32, 32>() : stream_kernel_ptr<DT, 32, 16>();
+    case 64: return t32 ? stream_kernel_ptr<DT, 64, 32>() : stream_kernel_ptr<DT, 64, 16>();
+    case 80: return t32 ? stream_kernel_ptr<DT, 80, 32>() : stream_kernel_ptr<DT, 80, 16>();
+    case 96: return t32 ? stream_kernel_ptr<DT, 96, 32>() : stream_kernel_ptr<DT, 96, 16>();
+    case 128: return t32 ? stream_kernel_ptr<DT, 128, 32>() : stream_kernel_ptr<DT, 128, 16>();
+    case 256: return t32 ? stream_kernel_ptr<DT, 256, 32>() : stream_kernel_ptr<DT, 256, 16>();
+    default: return nullptr;
   }
 }
 
 }  // namespace
 
-hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page,
-                         int blocks_per_wave, hipStream_t stream) {
-  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, blocks_per_wave, stream);
-  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, blocks_per_wave, stream);
+hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, int* workers) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  int cus = 0;
+  err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess) return err;
+  const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page)
+                                  : stream_kernel_for<kF16>(head_dim, tokens_per_page);
+  if (!fn) return hipErrorInvalidValue;
+  int groups_per_cu = 0;
+  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kWorkersPerGroup * kWave, 0);
+  if (err != hipSuccess) return err;
+  if (groups_per_cu < 1) groups_per_cu = 1;
+  *workers = cus * groups_per_cu * kWorkersPerGroup;
+  return hipSuccess;
+}
+
+hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream) {
+  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, stream);
+  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, stream);
 }
 
 }  // namespace pal

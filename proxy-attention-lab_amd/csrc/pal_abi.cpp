@@ -46,21 +46,53 @@ bool decode_head_dim_supported(int hd) {
   return hd == 32 || hd == 64 || hd == 80 || hd == 96 || hd == 128 || hd == 256;
 }
 
-// Partition size (tokens) -> 16-token blocks per wavefront (4 wavefronts).
-int blocks_per_wave_for(int partition_size) {
-  switch (partition_size) {
-    case 0: return 8;  // default: the reference's CHUNK_SIZE of 512 tokens
-    case 128: return 2;
-    case 256: return 4;
-    case 512: return 8;
-    default: return -1;
-  }
+bool decode_partition_ok(int partition_size) {
+  return partition_size == 0 || partition_size == 128 || partition_size == 256 || partition_size == 512;
 }
 
-int64_t decode_max_parts(int64_t page_table_width, int tokens_per_page, int bpw) {
-  const int64_t blocks = (page_table_width * tokens_per_page + 15) / 16;
-  const int64_t per_part = 4LL * bpw;
-  return (blocks + per_part - 1) / per_part;
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+// Decode workspace layout for a given worker count (all offsets 256-aligned).
+struct DecodeLayout {
+  size_t hdr, cum, plan, part_ml, part_o, total;
+};
+
+DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t workers) {
+  DecodeLayout l;
+  size_t off = 0;
+  l.hdr = off;
+  off += align256(2 * sizeof(int64_t));
+  l.cum = off;
+  off += align256(static_cast<size_t>(num_seqs + 1) * sizeof(int64_t));
+  l.plan = off;
+  off += align256(static_cast<size_t>(workers) * 2 * sizeof(int64_t));
+  l.part_ml = off;
+  off += align256(static_cast<size_t>(workers) * 2 * hg_max * 2 * sizeof(float));
+  l.part_o = off;
+  off += align256(static_cast<size_t>(workers) * 2 * hg_max * head_dim * sizeof(float));
+  l.total = off;
+  return l;
+}
+
+// Workers to launch: what the GPU keeps resident, or more when a partition
+// size caps the tokens per worker (bounded by the page-table capacity).
+int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seqs, int num_kv_heads,
+                   int head_chunks, int64_t page_table_width, int partition_size, int* resident, int* launched) {
+  int res = 0;
+  hipError_t err = pal::decode_resident_workers(dtype, head_dim, tokens_per_page, &res);
+  if (err != hipSuccess)
+    return fail(PAL_ERR_HIP, "[paged_attention_decode] occupancy query failed: %s", hipGetErrorString(err));
+  int64_t n = res;
+  if (partition_size > 0) {
+    const int64_t max_blocks =
+        num_seqs * ((page_table_width * tokens_per_page + 15) / 16) * num_kv_heads * head_chunks;
+    const int64_t want = (max_blocks * 16 + partition_size - 1) / partition_size;
+    if (want > n) n = want;
+  }
+  if (n > (1LL << 26)) return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] problem too large for one call");
+  *resident = res;
+  *launched = static_cast<int>(n);
+  return PAL_OK;
 }
 
 }  // namespace
@@ -135,17 +167,21 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
   return hip_status(pal::launch_fill_kv_pages(p, static_cast<hipStream_t>(stream)), "fill_kv_pages");
 }
 
-size_t pal_paged_attention_decode_workspace_size(int64_t num_seqs, int num_q_heads, int head_dim,
-                                                 int tokens_per_page, int64_t page_table_width,
-                                                 int partition_size) {
-  const int bpw = blocks_per_wave_for(partition_size);
-  if (bpw < 0 || num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
-      page_table_width <= 0)
+size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, int num_q_heads,
+                                                 int num_kv_heads, int head_dim, int tokens_per_page,
+                                                 int64_t page_table_width, int partition_size) {
+  if (!valid_dtype(dtype) || num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      tokens_per_page <= 0 || page_table_width < 0 || num_q_heads % num_kv_heads != 0 ||
+      !decode_partition_ok(partition_size) || !decode_head_dim_supported(head_dim) ||
+      (tokens_per_page != 16 && tokens_per_page != 32))
     return 0;
-  const int64_t parts = decode_max_parts(page_table_width, tokens_per_page, bpw);
-  if (parts <= 1) return 0;
-  const int64_t slots = num_seqs * num_q_heads * parts;
-  return static_cast<size_t>(slots) * (static_cast<size_t>(head_dim) + 2) * sizeof(float);
+  const int group = num_q_heads / num_kv_heads;
+  const int chunks = (group + 15) / 16;
+  int resident = 0, launched = 0;
+  if (decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
+                     partition_size, &resident, &launched) != PAL_OK)
+    return 0;
+  return decode_layout(num_seqs, head_dim, group < 16 ? group : 16, launched).total;
 }
 
 int pal_paged_attention_decode(const void* queries, const void* k_pool, const void* v_pool,
@@ -167,27 +203,33 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
     return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for head_dim %d (supported: 32, 64, 80, 96, 128, 256)", head_dim);
   if (tokens_per_page != 16 && tokens_per_page != 32)
     return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for tokens_per_page %d (supported: 16, 32)", tokens_per_page);
-  const int bpw = blocks_per_wave_for(partition_size);
-  if (bpw < 0)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] partition_size %d not in {0, 128, 256, 512}", partition_size);
+  if (!decode_partition_ok(partition_size))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] partition_size %d not in {0, 128, 256, 512}",
+                partition_size);
   if (num_query_rows < num_seqs)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] %lld query rows for %lld sequences",
                 static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs));
   if (num_seqs == 0) return ok();
-  if (num_seqs > 65535)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] at most 65535 sequences per call");
   if (!queries || !k_pool || !v_pool || !sequence_lengths || !out || (page_table_width > 0 && !page_table))
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] null pointer argument");
-  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] queries and pools must be 16-byte aligned");
-  const size_t need = pal_paged_attention_decode_workspace_size(
-      num_seqs, num_q_heads, head_dim, tokens_per_page, page_table_width, partition_size);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(PAL_ERR_INVALID_ARGUMENT,
+                "[paged_attention_decode] queries and pools must be 16-byte aligned, out 8-byte aligned");
+  const int group = num_q_heads / num_kv_heads;
+  const int chunks = (group + 15) / 16;
+  const int hg_max = group < 16 ? group : 16;
+  int resident = 0, launched = 0;
+  const int st = decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
+                                partition_size, &resident, &launched);
+  if (st != PAL_OK) return st;
+  const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, launched);
+  if (workspace == nullptr || workspace_bytes < lay.total)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace of %zu bytes needed, %zu given",
-                need, workspace_bytes);
-  if (need > 0 && !aligned16(workspace))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 16-byte aligned");
+                lay.total, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 256-byte aligned");
 
+  char* ws = static_cast<char*>(workspace);
   pal::DecodeParams p;
   p.q = static_cast<const uint16_t*>(queries);
   p.k_pool = static_cast<const uint16_t*>(k_pool);
@@ -195,19 +237,24 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
   p.page_table = page_table;
   p.seq_lens = sequence_lengths;
   p.out = static_cast<uint16_t*>(out);
-  const int64_t parts = page_table_width > 0 ? decode_max_parts(page_table_width, tokens_per_page, bpw) : 1;
-  p.max_parts = static_cast<int>(parts);
-  p.part_ml = static_cast<float*>(workspace);
-  p.part_o = need > 0 ? static_cast<float*>(workspace) + num_seqs * num_q_heads * parts * 2 : nullptr;
+  p.hdr = reinterpret_cast<int64_t*>(ws + lay.hdr);
+  p.cum = reinterpret_cast<int64_t*>(ws + lay.cum);
+  p.plan = reinterpret_cast<int64_t*>(ws + lay.plan);
+  p.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+  p.part_o = reinterpret_cast<float*>(ws + lay.part_o);
   p.num_seqs = num_seqs;
   p.num_pages = num_pages;
   p.page_table_width = page_table_width;
   p.num_q_heads = num_q_heads;
   p.num_kv_heads = num_kv_heads;
-  p.group = num_q_heads / num_kv_heads;
-  p.head_chunks = (p.group + 15) / 16;
+  p.group = group;
+  p.head_chunks = chunks;
+  p.hg_max = hg_max;
+  p.num_workers = launched;
+  p.min_workers = resident;
+  p.tokens_per_worker = partition_size;
   p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
-  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, bpw, static_cast<hipStream_t>(stream)),
+  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)),
                     "paged_attention_decode");
 }
 

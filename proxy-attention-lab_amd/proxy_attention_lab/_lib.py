@@ -43,7 +43,7 @@ _SIGNATURES = {
     ),
     "pal_paged_attention_decode_workspace_size": (
         _c_size_t,
-        [_c_i64, _c_int, _c_int, _c_int, _c_i64, _c_int],
+        [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int],
     ),
     "pal_paged_attention_decode": (
         _c_int,

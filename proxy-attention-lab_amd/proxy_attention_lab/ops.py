@@ -103,8 +103,9 @@ def paged_attention_decode(
     page_table: [S, W] uint32/int32; sequence_lengths: [S] int32.
     Returns [S, Hq, HD] in the query dtype (decode_primitive.cpp:289-300;
     the "[N*Hq, HD]" in the reference docstring does not match its code).
-    ``partition_size`` (keyword-only, 0 = 512) sets the tokens per split-K
-    partition: 128, 256 or 512.
+    ``partition_size`` (keyword-only): 0 spreads the KV blocks evenly over
+    the workers the GPU keeps resident; 128, 256 or 512 additionally caps the
+    tokens one worker reduces before the log-sum-exp merge.
     """
     _require_device("queries", queries)
     device = queries.device
@@ -142,10 +143,13 @@ def paged_attention_decode(
     vp = v_cache_pool.contiguous()
     out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=queries.dtype, device=device)
     L = _lib.lib()
-    ws_bytes = L.pal_paged_attention_decode_workspace_size(
-        num_seqs, num_q_heads, head_dim, tpp, width, int(partition_size)
-    )
-    ws = _workspace(ws_bytes, device)
+    ws = None
+    ws_bytes = 0
+    if num_seqs > 0:
+        with torch.cuda.device(device):
+            ws_bytes = L.pal_paged_attention_decode_workspace_size(
+                code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width, int(partition_size))
+        ws = _workspace(ws_bytes, device)
     status = L.pal_paged_attention_decode(
         _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
         code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,

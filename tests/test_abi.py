@@ -79,13 +79,13 @@ def test_decode_rejects_bad_arguments_without_launch():
         _lib.check(_lib.PAL_ERR_RUNTIME)
 
 
-def test_decode_workspace_size():
+def test_decode_workspace_size_rejects_bad_arguments():
     lib = _lib.lib()
-    # 4096 tokens in 512-token partitions -> 8 partials of (HD + 2) floats per (seq, q head)
-    assert lib.pal_paged_attention_decode_workspace_size(64, 32, 128, 16, 256, 0) == 64 * 32 * 8 * 130 * 4
-    assert lib.pal_paged_attention_decode_workspace_size(64, 32, 128, 16, 256, 256) == 64 * 32 * 16 * 130 * 4
-    # a single partition needs no workspace
-    assert lib.pal_paged_attention_decode_workspace_size(4, 4, 64, 16, 32, 512) == 0
+    # unsupported arguments report 0 bytes (no device is touched for them)
+    assert lib.pal_paged_attention_decode_workspace_size(5, 64, 32, 8, 128, 16, 256, 0) == 0  # dtype
+    assert lib.pal_paged_attention_decode_workspace_size(1, 64, 30, 8, 128, 16, 256, 0) == 0  # Hq % Hkv
+    assert lib.pal_paged_attention_decode_workspace_size(1, 64, 32, 8, 48, 16, 256, 0) == 0  # head_dim
+    assert lib.pal_paged_attention_decode_workspace_size(1, 64, 32, 8, 128, 16, 256, 100) == 0  # partition
 
 
 def test_ops_reject_host_tensors_and_bad_ranks():

@@ -151,3 +151,13 @@ def test_decode_llama3_8b_shape_subset():
     sub = compact_subset(case, pick)
     ref = orc.paged_attention_decode(q[pick], sub.k_pool, sub.v_pool, sub.page_table, sub.seq_lens, "bf16")
     assert_close(out[pick], ref, "bf16", "config-2 subset")
+
+
+def test_decode_many_short_sequences():
+    """More sequences than the in-kernel planner takes (1024): the plan comes
+    from the separate plan kernel; lengths include zeros."""
+    rng = np.random.default_rng(15)
+    lens = rng.integers(0, 60, size=1500).astype(np.int32)
+    case = make_paged_case(15, lens, 8, 2, 64, 16, "bf16", garbage_tail=False)
+    q = randn_bits(rng, (1500, 8, 64), "bf16")
+    _check(case, q, what="1500 sequences")
