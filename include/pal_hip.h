@@ -85,12 +85,17 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
 /*
  * Workspace bytes pal_paged_attention_decode needs for these shapes on the
  * current device (0 for unsupported arguments or when no device is present).
- * The workspace holds the work plan and the fp32 partials (max, exp-sum,
- * unnormalised output) of KV segments split between workers; its size
- * follows from the number of workers the device keeps resident.
- * partition_size: 0 (default: one equal share of the KV blocks per resident
- * worker) or 128 / 256 / 512, a cap on the tokens one worker reduces (the
- * reference's CHUNK_SIZE is 512, paged_attention_types.h:33).
+ * The workspace holds a scan of the sequence lengths, a work-claim counter
+ * and the fp32 partials (max, exp-sum, unnormalised output) of KV segments
+ * split between workers; its size follows from the number of wavefront
+ * workers the device keeps resident.
+ * partition_size: 0 (default: the KV blocks of the batch are shared out
+ * evenly, three quarters statically and the rest in small chunks claimed by
+ * whichever worker is free) or 128 / 256 / 512: fixed chunks of that many
+ * tokens, each merged by log-sum-exp (the reference's CHUNK_SIZE is 512,
+ * paged_attention_types.h:33).
+ * The workspace must be zero-filled before its first use; each call leaves
+ * it ready for the next one on the same stream.
  */
 size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, int num_q_heads,
                                                  int num_kv_heads, int head_dim, int tokens_per_page,
@@ -109,8 +114,9 @@ size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, in
  * resident workers; a sequence split between workers is merged with a
  * log-sum-exp pass (the reference's two-pass mode,
  * decode_primitive.cpp:100-102,163-240) from fp32 partials.  The workspace
- * (256-byte aligned, size from pal_paged_attention_decode_workspace_size)
- * must not be shared by concurrent calls.
+ * (256-byte aligned, size from pal_paged_attention_decode_workspace_size,
+ * zero-filled before its first use) must not be shared by calls that can
+ * run concurrently.
  */
 int pal_paged_attention_decode(const void* queries, const void* k_pool, const void* v_pool,
                                const uint32_t* page_table, const int32_t* sequence_lengths,

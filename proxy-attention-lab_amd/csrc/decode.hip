@@ -1,5 +1,8 @@
-// Paged-attention decode for gfx950: balanced ("stream-K") split of the KV
-// stream over a resident set of wavefront workers, then a log-sum-exp merge.
+// Paged-attention decode for gfx950: the KV stream of the whole batch is split
+// into 16-token blocks, shared out to a resident set of wavefront workers
+// (three quarters statically, the rest claimed dynamically in small chunks),
+// and the pieces of sequences that several workers shared are merged with a
+// log-sum-exp pass.
 //
 // Reference behaviour: kernels/paged_attention/decode/paged_attention_decode.h.metal
 // (one query row per sequence, GQA map h -> h / (Hq/Hkv) at :64-65, scale
@@ -11,13 +14,16 @@
 //    a run of 16-token blocks (one page for TPP=16, half a page for TPP=32).
 //    All query heads sharing a kv head (up to 16 per chunk) are processed
 //    together, so a K/V page block is read from HBM once per GQA group.
-//  * The sequence lengths are scanned (by every worker itself for batches of
-//    up to 1024 sequences, else by decode_plan_kernel) and every worker (one
-//    wavefront) gets an equal share of the total blocks: worker w owns global
-//    blocks [w*T/NW, (w+1)*T/NW).  Every worker therefore streams
-//    the same number of bytes and the grid drains evenly -- no tail of
-//    half-empty partitions.  NW is sized to what the GPU keeps resident.
-//  * A worker streams its blocks with a software pipeline: the K and V loads
+//  * The global block list [0, T) is cut into "virtual workers": equal
+//    static ranges (one per resident wavefront) and, in the fixed-chunk mode
+//    (partition_size > 0) or when a static share below 1 is compiled in,
+//    chunks of C blocks that wavefronts claim from an atomic counter once
+//    their static range is done.  Because the cut is fixed, which wavefront
+//    computes a chunk changes nothing in the result.
+//  * Each workgroup scans the sequence lengths into LDS (batches of up to
+//    1024 sequences; larger ones are scanned once by decode_plan_kernel into
+//    the workspace) and locates the sequence of a range by binary search.
+//  * A wavefront streams blocks with a software pipeline: the K and V loads
 //    of the next PF blocks are in flight while the current block is computed.
 //    The K block is read in the pool's striped [HD/8][TPP][8] layout, which is
 //    exactly the A operand of v_mfma_f32_16x16x32 for S^T = K * Q^T (lane l
@@ -27,14 +33,14 @@
 //    O^T = V^T * P^T; V is read as 8-byte runs of 4 tokens from the [HD][TPP]
 //    layout as its A operand.  In O^T the head is the lane, so the online
 //    softmax rescale is a per-lane multiply.
-//  * A segment that lies wholly inside one worker writes the normalised output
-//    directly.  Segments split across workers leave fp32 partials
-//    (max, exp-sum, unnormalised O) in one of two slots per worker, combined
-//    by decode_merge_kernel.
+//  * A segment that lies wholly inside one virtual worker writes the
+//    normalised output directly.  Split segments leave fp32 partials
+//    (max, exp-sum, unnormalised O) in one of two slots per virtual worker,
+//    combined by decode_merge_kernel, which also re-arms the claim counter.
 #include "pal_device.h"
 
 #ifndef PAL_DECODE_PREFETCH
-#define PAL_DECODE_PREFETCH 2  // blocks whose loads are in flight ahead of the one being computed
+#define PAL_DECODE_PREFETCH 3  // blocks whose loads are in flight ahead of the one being computed
 #endif
 
 namespace pal {
@@ -42,8 +48,14 @@ namespace pal {
 namespace {
 
 constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
+constexpr int kGroupThreads = kWorkersPerGroup * kWave;
 constexpr int kPlanThreads = 1024;
-constexpr int kInlinePlanSeqs = 1024;  // largest batch planned inside the stream kernel
+constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each workgroup
+#ifndef PAL_DECODE_STATIC_SHARE
+#define PAL_DECODE_STATIC_SHARE 4  // static quarters of the block list (4 = all static)
+#endif
+constexpr int64_t kStaticShareNum = PAL_DECODE_STATIC_SHARE;
+constexpr int64_t kStaticShareDen = 4;
 
 __device__ __forceinline__ int64_t seq_blocks(const DecodeParams& p, int64_t s, int tpp) {
   const int64_t max_tokens = p.page_table_width * tpp;
@@ -52,14 +64,62 @@ __device__ __forceinline__ int64_t seq_blocks(const DecodeParams& p, int64_t s, 
   return (len + 15) >> 4;
 }
 
-__device__ __forceinline__ int64_t worker_start(int64_t w, int64_t total, int64_t nw) { return (w * total) / nw; }
+// The fixed cut of the global block list into virtual workers.
+struct Sched {
+  int64_t total;  // T: blocks of all segments
+  int64_t ts;     // static region [0, ts), split evenly over nws workers
+  int64_t nws;    // static virtual workers: min(resident workers, ts), so none is empty
+  int64_t chunk;  // blocks per dynamic chunk
+  int64_t nc;     // dynamic chunks covering [ts, total); virtual ids nws .. nws + nc - 1
+};
 
-// Worker that owns global block b (total > 0).
-__device__ __forceinline__ int64_t worker_of(int64_t b, int64_t total, int64_t nw) {
-  return ((b + 1) * nw + total - 1) / total - 1;
+__device__ __forceinline__ Sched make_sched(int64_t total, int64_t nw, int tokens_per_worker) {
+  Sched sc;
+  sc.total = total;
+  if (tokens_per_worker > 0) {  // fixed-size chunks only (the reference's CHUNK_SIZE mode)
+    sc.ts = 0;
+    sc.chunk = tokens_per_worker / 16 > 0 ? tokens_per_worker / 16 : 1;
+  } else {
+    // Static shares only.  (A dynamically claimed tail would absorb the
+    // uneven finish of the shares, but each claimed range restarts the load
+    // pipeline; until ranges are chained without that bubble, small chunks
+    // cost more than they balance.)
+    sc.ts = total * kStaticShareNum / kStaticShareDen;
+    const int64_t dyn = total - sc.ts;
+    sc.chunk = (dyn + 4 * nw - 1) / (4 * nw);  // about four chunks per worker
+    if (sc.chunk < 1) sc.chunk = 1;
+  }
+  sc.nws = sc.ts < nw ? sc.ts : nw;
+  sc.nc = (total - sc.ts + sc.chunk - 1) / sc.chunk;
+  return sc;
 }
 
-// Block-wide inclusive scan of int64 values (blockDim.x == kPlanThreads).
+// First global block of virtual worker v (v in [0, nws + nc]); every virtual
+// worker owns at least one block.
+__device__ __forceinline__ int64_t vstart(const Sched& sc, int64_t v) {
+  if (v <= sc.nws) return sc.nws > 0 ? (v * sc.ts) / sc.nws : 0;
+  const int64_t b = sc.ts + (v - sc.nws) * sc.chunk;
+  return b < sc.total ? b : sc.total;
+}
+
+// Virtual worker whose range holds global block b.
+__device__ __forceinline__ int64_t vworker_of(const Sched& sc, int64_t b) {
+  if (b < sc.ts) return ((b + 1) * sc.nws + sc.ts - 1) / sc.ts - 1;
+  return sc.nws + (b - sc.ts) / sc.chunk;
+}
+
+// Sequence holding global block b: the largest s with cum[s] <= b.
+__device__ __forceinline__ int64_t locate_seq(const int64_t* cum, int64_t num_seqs, int64_t b) {
+  int64_t lo = 0, hi = num_seqs - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (cum[mid] <= b) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Block-wide inclusive scan of int64 values over `threads` threads.
+template <int kThreads>
 __device__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_sums) {
   const int lane = lane_id();
   const int wv = static_cast<int>(threadIdx.x) >> 6;
@@ -76,139 +136,41 @@ __device__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_sums) {
   return v + add;
 }
 
-// Scans the sequence lengths: cum[s] = first global block of sequence s (all
-// of its segments), hdr = {T, NW_eff}, plan[w] = {sequence, block offset in
-// that sequence's segments} of worker w's first block.
+// Scan for batches larger than kInlinePlanSeqs: cum[s] = first global block of
+// sequence s (all of its segments), cum[S] = hdr[0] = T.
 template <int TPP>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeParams p) {
   __shared__ int64_t wave_sums[kPlanThreads / kWave];
-  __shared__ int64_t total_sh;
+  __shared__ int64_t carry_sh;
   const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
   const int tid = threadIdx.x;
-
-  int64_t local = 0;
-  for (int64_t s = tid; s < p.num_seqs; s += kPlanThreads) local += seq_blocks(p, s, TPP) * segs;
-  const int64_t incl = block_inclusive_scan(local, wave_sums);
-  if (tid == kPlanThreads - 1) total_sh = incl;
-  __syncthreads();
-  const int64_t total = total_sh;
-  int64_t nw = p.num_workers;
-  if (p.tokens_per_worker > 0) {
-    int64_t want = (total * 16 + p.tokens_per_worker - 1) / p.tokens_per_worker;
-    if (want < p.min_workers) want = p.min_workers;
-    if (want < nw) nw = want;
-  }
-  if (nw > total) nw = total > 0 ? total : 1;
-  if (tid == 0) {
-    p.hdr[0] = total;
-    p.hdr[1] = nw;
-  }
-
   int64_t carry = 0;
   for (int64_t base = 0; base < p.num_seqs; base += kPlanThreads) {
     const int64_t s = base + tid;
     const int64_t v = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
-    const int64_t inc = block_inclusive_scan(v, wave_sums);
-    const int64_t start = carry + inc - v;
-    if (s < p.num_seqs) {
-      p.cum[s] = start;
-      if (v > 0) {
-        // workers whose first block falls in [start, start + v)
-        const int64_t wa = (start * nw + total - 1) / total;
-        const int64_t wb = ((start + v) * nw + total - 1) / total;
-        for (int64_t w = wa; w < wb; ++w) {
-          p.plan[2 * w + 0] = s;
-          p.plan[2 * w + 1] = worker_start(w, total, nw) - start;
-        }
-      }
-    }
-    if (tid == kPlanThreads - 1) total_sh = inc;
+    const int64_t inc = block_inclusive_scan<kPlanThreads>(v, wave_sums);
+    if (s < p.num_seqs) p.cum[s] = carry + inc - v;
+    if (tid == kPlanThreads - 1) carry_sh = inc;
     __syncthreads();
-    carry += total_sh;
+    carry += carry_sh;
     __syncthreads();
   }
-  if (tid == 0) p.cum[p.num_seqs] = total;
+  if (tid == 0) {
+    p.cum[p.num_seqs] = carry;
+    p.hdr[0] = carry;
+  }
 }
 
-// Plan computed by one wavefront from the sequence lengths (S <= kInlinePlanSeqs):
-// lane l sums the blocks of sequences [16 l, 16 l + 16), a wave scan gives
-// every lane's first global block, and the lane whose range holds block b0
-// walks its sequences to find the one containing it.  The worker with id 0
-// also stores hdr and cum[] for the merge kernel.
-struct WavePlan {
-  int64_t total;  // T
-  int64_t nw;     // workers in use
-  int64_t s;      // sequence of the worker's first block
-  int64_t r;      // its block offset within that sequence's segments
-};
+#ifdef PAL_DECODE_WAVES_PER_EU
+#define PAL_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(PAL_DECODE_WAVES_PER_EU, PAL_DECODE_WAVES_PER_EU)))
+#else
+#define PAL_DECODE_OCCUPANCY
+#endif
 
-template <int TPP>
-__device__ WavePlan wave_plan(const DecodeParams& p, int64_t w) {
-  constexpr int K = kInlinePlanSeqs / kWave;
-  const int lane = lane_id();
-  const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
-  int64_t nb[K];
-  int64_t lane_sum = 0;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int64_t s = static_cast<int64_t>(lane) * K + k;
-    nb[k] = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
-    lane_sum += nb[k];
-  }
-  int64_t incl = lane_sum;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int64_t o = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += o;
-  }
-  const int64_t excl = incl - lane_sum;
-  WavePlan wp;
-  wp.total = __shfl(incl, kWave - 1, kWave);
-  int64_t nw = p.num_workers;
-  if (p.tokens_per_worker > 0) {
-    int64_t want = (wp.total * 16 + p.tokens_per_worker - 1) / p.tokens_per_worker;
-    if (want < p.min_workers) want = p.min_workers;
-    if (want < nw) nw = want;
-  }
-  if (nw > wp.total) nw = wp.total > 0 ? wp.total : 1;
-  wp.nw = nw;
-  if (w == 0) {
-    int64_t c = excl;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int64_t s = static_cast<int64_t>(lane) * K + k;
-      if (s < p.num_seqs) p.cum[s] = c;
-      c += nb[k];
-    }
-    if (lane == 0) {
-      p.hdr[0] = wp.total;
-      p.hdr[1] = nw;
-      p.cum[p.num_seqs] = wp.total;
-    }
-  }
-  wp.s = 0;
-  wp.r = 0;
-  if (wp.total == 0 || w >= nw) return wp;
-  const int64_t b0 = worker_start(w, wp.total, nw);
-  const uint64_t owner = __ballot(lane_sum > 0 && excl <= b0 && b0 < incl);
-  const int L = __builtin_ctzll(owner);
-  int64_t s_found = 0, r_found = 0;
-  int64_t c = excl;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    if (s_found == 0 && r_found == 0 && b0 >= c && b0 < c + nb[k]) {
-      s_found = static_cast<int64_t>(lane) * K + k + 1;  // +1: 0 means "not found yet"
-      r_found = b0 - c;
-    }
-    c += nb[k];
-  }
-  wp.s = __shfl(s_found, L, kWave) - 1;
-  wp.r = __shfl(r_found, L, kWave);
-  return wp;
-}
-
+// Streams the blocks of virtual worker v (one wavefront).
 template <int DT, int HD, int TPP>
-__global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel(const DecodeParams p) {
+__device__ __forceinline__ void process_range(const DecodeParams& p, const Sched& sc, const int64_t* cum,
+                                              int64_t v) {
   constexpr bool kK32 = (HD % 32) == 0;  // QK k-step of 32 (else 16)
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
   constexpr int NT = HD / 16;            // output tiles of 16 dims
@@ -218,25 +180,11 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel
   // whatever the alignment of the first block within its page.
   constexpr int kChunkBlocks = (kWave - 1) * TPP / 16;
 
-  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  int64_t total, nw, s, r;
-  if (p.num_seqs <= kInlinePlanSeqs) {
-    const WavePlan wp = wave_plan<TPP>(p, w);
-    total = wp.total;
-    nw = wp.nw;
-    s = wp.s;
-    r = wp.r;
-  } else {  // planned by decode_plan_kernel
-    total = p.hdr[0];
-    nw = p.hdr[1];
-    if (w >= nw || total == 0) return;
-    s = p.plan[2 * w + 0];
-    r = p.plan[2 * w + 1];
-  }
-  if (w >= nw || total == 0) return;
-  const int64_t b0 = worker_start(w, total, nw);
-  int64_t remaining = worker_start(w + 1, total, nw) - b0;
+  const int64_t b0 = vstart(sc, v);
+  int64_t remaining = vstart(sc, v + 1) - b0;
   if (remaining <= 0) return;
+  int64_t s = locate_seq(cum, p.num_seqs, b0);
+  int64_t r = b0 - cum[s];
 
   const int lane = lane_id();
   const int g = lane >> 4;
@@ -344,12 +292,12 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel
         }
         // tokens past the end (and whole invalid blocks) are masked
         const int64_t t0 = live ? b * 16 + 4 * g : len;
-        float sc[4];
+        float sc4[4];
         float bm = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          sc[e] = (t0 + e < len) ? acc[e] : -INFINITY;
-          bm = fmaxf(bm, sc[e]);
+          sc4[e] = (t0 + e < len) ? acc[e] : -INFINITY;
+          bm = fmaxf(bm, sc4[e]);
         }
         bm = fmaxf(bm, shfl_xor(bm, 16));
         bm = fmaxf(bm, shfl_xor(bm, 32));
@@ -366,7 +314,7 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel
         float pe[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pe[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], p.scale_log2, -msc));
+          pe[e] = __builtin_amdgcn_exp2f(fmaf(sc4[e], p.scale_log2, -msc));
           l_run += pe[e];
         }
         const u32x2 pb = {Dt<DT>::pack2(pe[0], pe[1]), Dt<DT>::pack2(pe[2], pe[3])};
@@ -397,7 +345,7 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel
       }
     }
 
-    // ---- finish the segment: exp-sum of head r16 across the 4 lane groups --
+    // ---- finish the segment piece: exp-sum of head r16 over the 4 lane groups
     float l = l_run;
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
@@ -411,7 +359,7 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel
           *reinterpret_cast<u32x2*>(p.out + row * HD + 16 * n + 4 * g) = pk;
         }
       } else {
-        const int64_t slot = (w * 2 + (first ? 0 : 1)) * p.hg_max + r16;
+        const int64_t slot = (v * 2 + (first ? 0 : 1)) * p.hg_max + r16;
 #pragma unroll
         for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(p.part_o + slot * HD + 16 * n + 4 * g) = o[n];
         if (g == 0) {
@@ -431,14 +379,70 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_stream_kernel
   }
 }
 
-// One wavefront per (sequence, query head): combines the partials of a
-// segment that several workers shared, M = max_c m_c,
-// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  Lane j fetches the
-// (m, l) of the j-th contributing worker so those loads go out together; the
-// O loads of consecutive workers are unrolled to keep several in flight.
-// Empty sequences get zeros; segments finished by one worker are already out.
 template <int DT, int HD, int TPP>
-__global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_merge_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(kGroupThreads) PAL_DECODE_OCCUPANCY
+void decode_stream_kernel(const DecodeParams p) {
+  __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
+  __shared__ int64_t wave_sums[kWorkersPerGroup];
+  const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
+  const int64_t* cum = p.cum;
+  int64_t total = 0;
+  if (lds_plan) {
+    // Every workgroup scans the (at most 1024) sequence lengths into LDS:
+    // thread t owns sequences 4t .. 4t+3.
+    constexpr int kPer = kInlinePlanSeqs / kGroupThreads;
+    const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
+    const int tid = threadIdx.x;
+    int64_t vals[kPer];
+    int64_t tsum = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int64_t s = static_cast<int64_t>(tid) * kPer + k;
+      vals[k] = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
+      tsum += vals[k];
+    }
+    const int64_t incl = block_inclusive_scan<kGroupThreads>(tsum, wave_sums);
+    int64_t c = incl - tsum;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int64_t s = static_cast<int64_t>(tid) * kPer + k;
+      if (s < p.num_seqs) cum_lds[s] = c;
+      c += vals[k];
+    }
+    if (tid == kGroupThreads - 1) cum_lds[p.num_seqs] = incl;
+    __syncthreads();
+    total = cum_lds[p.num_seqs];
+    if (blockIdx.x == 0) {  // the merge kernel reads the scan from the workspace
+      for (int64_t s = tid; s <= p.num_seqs; s += kGroupThreads) p.cum[s] = cum_lds[s];
+      if (tid == 0) p.hdr[0] = total;
+    }
+    cum = cum_lds;
+  } else {
+    total = p.hdr[0];
+  }
+  if (total == 0) return;
+  const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
+  if (w < sc.nws) process_range<DT, HD, TPP>(p, sc, cum, w);
+  while (sc.nc > 0) {
+    uint32_t k = 0;
+    if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
+    k = __builtin_amdgcn_readfirstlane(k);
+    if (k >= sc.nc) break;
+    process_range<DT, HD, TPP>(p, sc, cum, sc.nws + k);
+  }
+}
+
+// One wavefront per (sequence, query head): combines the partials of a
+// segment that several virtual workers shared, M = max_c m_c,
+// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  Lane j fetches the
+// (m, l) of the j-th contributor so those loads go out together; the O loads
+// of consecutive contributors are unrolled to keep several in flight.
+// Empty sequences get zeros; segments finished by one worker are already out.
+// The first thread re-arms the claim counter for the next call.
+template <int DT, int HD, int TPP>
+__global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
   if (row >= p.num_seqs * p.num_q_heads) return;
   const int64_t s = row / p.num_q_heads;
@@ -447,7 +451,6 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_merge_kernel(
   constexpr int kPer = (HD + kWave - 1) / kWave;
   const int64_t nb = seq_blocks(p, s, TPP);
   const int64_t total = p.hdr[0];
-  const int64_t nw = p.hdr[1];
   const int64_t cum_s = p.cum[s];
   if (nb == 0) {
 #pragma unroll
@@ -457,23 +460,23 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_merge_kernel(
     }
     return;
   }
+  const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
   const int kvh = qh / p.group;
   const int hl = qh - kvh * p.group;
   const int seg = kvh * p.head_chunks + hl / 16;
   const int h = hl % 16;
   const int64_t g0 = cum_s + seg * nb;
-  const int64_t g1 = g0 + nb;
-  const int64_t w0 = worker_of(g0, total, nw);
-  const int64_t w1 = worker_of(g1 - 1, total, nw);
-  if (w0 == w1) return;
-  const int64_t n = w1 - w0 + 1;
+  const int64_t v0 = vworker_of(sc, g0);
+  const int64_t v1 = vworker_of(sc, g0 + nb - 1);
+  if (v0 == v1) return;
+  const int64_t n = v1 - v0 + 1;
 
-  auto slot_of = [&](int64_t w) { return (w * 2 + (worker_start(w, total, nw) >= g0 ? 0 : 1)) * p.hg_max + h; };
+  auto slot_of = [&](int64_t u) { return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h; };
 
   float big_m = -INFINITY;
   for (int64_t base = 0; base < n; base += kWave) {
     const int64_t j = base + lane;
-    const float m = j < n ? p.part_ml[slot_of(w0 + j) * 2] : -INFINITY;
+    const float m = j < n ? p.part_ml[slot_of(v0 + j) * 2] : -INFINITY;
     big_m = fmaxf(big_m, m);
   }
 #pragma unroll
@@ -488,7 +491,7 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_merge_kernel(
     const int64_t j = base + lane;
     float wgt = 0.f;
     if (j < n) {
-      const int64_t sl = slot_of(w0 + j);
+      const int64_t sl = slot_of(v0 + j);
       wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
       lsum += wgt * p.part_ml[sl * 2 + 1];
     }
@@ -496,7 +499,7 @@ __global__ __launch_bounds__(kWorkersPerGroup * kWave) void decode_merge_kernel(
 #pragma unroll 8
     for (int jj = 0; jj < cnt; ++jj) {
       const float wj = __shfl(wgt, jj, kWave);
-      const float* po = p.part_o + slot_of(w0 + base + jj) * HD;
+      const float* po = p.part_o + slot_of(v0 + base + jj) * HD;
 #pragma unroll
       for (int e = 0; e < kPer; ++e) {
         const int d = lane + e * kWave;
@@ -523,14 +526,14 @@ hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     if (err != hipSuccess) return err;
   }
   const int64_t groups = (static_cast<int64_t>(p.num_workers) + kWorkersPerGroup - 1) / kWorkersPerGroup;
-  hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)),
-                     dim3(kWorkersPerGroup * kWave), 0, stream, p);
+  hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)), dim3(kGroupThreads),
+                     0, stream, p);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int64_t rows = p.num_seqs * p.num_q_heads;
   hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>),
                      dim3(static_cast<unsigned>((rows + kWorkersPerGroup - 1) / kWorkersPerGroup)),
-                     dim3(kWorkersPerGroup * kWave), 0, stream, p);
+                     dim3(kGroupThreads), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -588,7 +591,7 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
                                   : stream_kernel_for<kF16>(head_dim, tokens_per_page);
   if (!fn) return hipErrorInvalidValue;
   int groups_per_cu = 0;
-  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kWorkersPerGroup * kWave, 0);
+  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kGroupThreads, 0);
   if (err != hipSuccess) return err;
   if (groups_per_cu < 1) groups_per_cu = 1;
   *workers = cus * groups_per_cu * kWorkersPerGroup;

@@ -52,46 +52,51 @@ bool decode_partition_ok(int partition_size) {
 
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
-// Decode workspace layout for a given worker count (all offsets 256-aligned).
+// Decode workspace layout (all offsets 256-aligned).  The claim counter at
+// byte 64 must be zero when a call starts; every call leaves it zero.
 struct DecodeLayout {
-  size_t hdr, cum, plan, part_ml, part_o, total;
+  size_t hdr, claim, cum, part_ml, part_o, total;
 };
 
-DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t workers) {
+DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t virtual_workers) {
   DecodeLayout l;
   size_t off = 0;
   l.hdr = off;
-  off += align256(2 * sizeof(int64_t));
+  l.claim = off + 64;
+  off += 256;
   l.cum = off;
   off += align256(static_cast<size_t>(num_seqs + 1) * sizeof(int64_t));
-  l.plan = off;
-  off += align256(static_cast<size_t>(workers) * 2 * sizeof(int64_t));
   l.part_ml = off;
-  off += align256(static_cast<size_t>(workers) * 2 * hg_max * 2 * sizeof(float));
+  off += align256(static_cast<size_t>(virtual_workers) * 2 * hg_max * 2 * sizeof(float));
   l.part_o = off;
-  off += align256(static_cast<size_t>(workers) * 2 * hg_max * head_dim * sizeof(float));
+  off += align256(static_cast<size_t>(virtual_workers) * 2 * hg_max * head_dim * sizeof(float));
   l.total = off;
   return l;
 }
 
-// Workers to launch: what the GPU keeps resident, or more when a partition
-// size caps the tokens per worker (bounded by the page-table capacity).
+// Resident wavefront workers, and the number of virtual workers (partial
+// slots) the cut can produce: static shares plus at most four dynamic chunks
+// per worker, or, with a partition size, one chunk per partition of the
+// page-table capacity.
 int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seqs, int num_kv_heads,
-                   int head_chunks, int64_t page_table_width, int partition_size, int* resident, int* launched) {
+                   int head_chunks, int64_t page_table_width, int partition_size, int* resident,
+                   int64_t* virtual_workers) {
   int res = 0;
   hipError_t err = pal::decode_resident_workers(dtype, head_dim, tokens_per_page, &res);
   if (err != hipSuccess)
     return fail(PAL_ERR_HIP, "[paged_attention_decode] occupancy query failed: %s", hipGetErrorString(err));
-  int64_t n = res;
+  int64_t vw;
   if (partition_size > 0) {
     const int64_t max_blocks =
         num_seqs * ((page_table_width * tokens_per_page + 15) / 16) * num_kv_heads * head_chunks;
-    const int64_t want = (max_blocks * 16 + partition_size - 1) / partition_size;
-    if (want > n) n = want;
+    const int64_t chunk = partition_size / 16;
+    vw = res + (max_blocks + chunk - 1) / chunk;
+  } else {
+    vw = 5LL * res + 1;
   }
-  if (n > (1LL << 26)) return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] problem too large for one call");
+  if (vw > (1LL << 28)) return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] problem too large for one call");
   *resident = res;
-  *launched = static_cast<int>(n);
+  *virtual_workers = vw;
   return PAL_OK;
 }
 
@@ -177,11 +182,12 @@ size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, in
     return 0;
   const int group = num_q_heads / num_kv_heads;
   const int chunks = (group + 15) / 16;
-  int resident = 0, launched = 0;
+  int resident = 0;
+  int64_t vw = 0;
   if (decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                     partition_size, &resident, &launched) != PAL_OK)
+                     partition_size, &resident, &vw) != PAL_OK)
     return 0;
-  return decode_layout(num_seqs, head_dim, group < 16 ? group : 16, launched).total;
+  return decode_layout(num_seqs, head_dim, group < 16 ? group : 16, vw).total;
 }
 
 int pal_paged_attention_decode(const void* queries, const void* k_pool, const void* v_pool,
@@ -218,11 +224,12 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
   const int group = num_q_heads / num_kv_heads;
   const int chunks = (group + 15) / 16;
   const int hg_max = group < 16 ? group : 16;
-  int resident = 0, launched = 0;
+  int resident = 0;
+  int64_t vw = 0;
   const int st = decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                                partition_size, &resident, &launched);
+                                partition_size, &resident, &vw);
   if (st != PAL_OK) return st;
-  const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, launched);
+  const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, vw);
   if (workspace == nullptr || workspace_bytes < lay.total)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace of %zu bytes needed, %zu given",
                 lay.total, workspace_bytes);
@@ -238,8 +245,8 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
   p.seq_lens = sequence_lengths;
   p.out = static_cast<uint16_t*>(out);
   p.hdr = reinterpret_cast<int64_t*>(ws + lay.hdr);
+  p.claim = reinterpret_cast<uint32_t*>(ws + lay.claim);
   p.cum = reinterpret_cast<int64_t*>(ws + lay.cum);
-  p.plan = reinterpret_cast<int64_t*>(ws + lay.plan);
   p.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
   p.part_o = reinterpret_cast<float*>(ws + lay.part_o);
   p.num_seqs = num_seqs;
@@ -250,8 +257,7 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
   p.group = group;
   p.head_chunks = chunks;
   p.hg_max = hg_max;
-  p.num_workers = launched;
-  p.min_workers = resident;
+  p.num_workers = resident;
   p.tokens_per_worker = partition_size;
   p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
   return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)),

@@ -30,9 +30,10 @@ struct FillParams {
 
 hipError_t launch_fill_kv_pages(const FillParams& p, hipStream_t stream);
 
-// Decode ("stream-K"): a plan kernel splits the flat list of 16-token blocks
-// of all (sequence, kv head, head chunk) segments evenly over num_workers
-// wavefront workers; a merge kernel combines segments shared by workers.
+// Decode: the flat list of 16-token blocks of all (sequence, kv head, head
+// chunk) segments is cut into virtual workers (static shares of the resident
+// wavefronts plus dynamically claimed chunks); a merge kernel combines the
+// segments that several virtual workers shared.
 struct DecodeParams {
   const uint16_t* q;           // [>=S, Hq, HD]
   const uint16_t* k_pool;      // [P, Hkv, HD/8, TPP, 8]
@@ -41,11 +42,11 @@ struct DecodeParams {
   const int32_t* seq_lens;     // [S]
   uint16_t* out;               // [S, Hq, HD]
   // workspace
-  int64_t* hdr;                // {total blocks T, workers in use}
+  int64_t* hdr;                // hdr[0] = total blocks T
+  uint32_t* claim;             // dynamic-chunk counter: 0 on entry, re-armed to 0 by the merge kernel
   int64_t* cum;                // [S + 1] first global block of each sequence
-  int64_t* plan;               // [num_workers][2] {sequence, block offset} of each worker's first block
-  float* part_ml;              // [num_workers][2][hg_max][2] (max * log2e * scale, exp-sum)
-  float* part_o;               // [num_workers][2][hg_max][HD]  unnormalised O
+  float* part_ml;              // [virtual workers][2][hg_max][2] (max * log2e * scale, exp-sum)
+  float* part_o;               // [virtual workers][2][hg_max][HD]  unnormalised O
   int64_t num_seqs;
   int64_t num_pages;
   int64_t page_table_width;
@@ -54,9 +55,8 @@ struct DecodeParams {
   int group;              // Hq / Hkv
   int head_chunks;        // ceil(group / 16)
   int hg_max;             // min(group, 16): query heads per segment
-  int num_workers;        // workers launched
-  int min_workers;        // workers the GPU keeps resident
-  int tokens_per_worker;  // cap on tokens per worker (0 = none)
+  int num_workers;        // resident wavefront workers launched
+  int tokens_per_worker;  // 0: static shares + dynamic chunks; > 0: fixed chunks of this many tokens
   float scale_log2;       // log2(e) / sqrt(HD)
 };
 

@@ -71,10 +71,27 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(nbytes: int, device: torch.device, stream_handle: int) -> torch.Tensor | None:
+    """Persistent, zero-initialised workspace per (device, stream).
+
+    The decode kernels keep a work-claim counter in it that must read zero
+    when a call starts; every call leaves it zero again, so the buffer is
+    reused as is by the next call on the same stream (calls on one stream
+    never overlap).  A larger request replaces it with a new zeroed buffer.
+    """
     if nbytes <= 0:
         return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        # the zero fill ran on torch's current stream; the kernels may use another
+        torch.cuda.current_stream(device).synchronize()
+        _WORKSPACES[key] = ws
+    return ws
 
 
 # ---------------------------------------------------------------------------
@@ -103,9 +120,11 @@ def paged_attention_decode(
     page_table: [S, W] uint32/int32; sequence_lengths: [S] int32.
     Returns [S, Hq, HD] in the query dtype (decode_primitive.cpp:289-300;
     the "[N*Hq, HD]" in the reference docstring does not match its code).
-    ``partition_size`` (keyword-only): 0 spreads the KV blocks evenly over
-    the workers the GPU keeps resident; 128, 256 or 512 additionally caps the
-    tokens one worker reduces before the log-sum-exp merge.
+    ``partition_size`` (keyword-only): 0 shares the KV blocks of the batch
+    out to the workers the GPU keeps resident (three quarters statically, the
+    rest claimed in small chunks by whichever worker is free); 128, 256 or 512
+    splits the KV stream into fixed chunks of that many tokens instead, merged
+    by log-sum-exp as in the reference's two-pass mode.
     """
     _require_device("queries", queries)
     device = queries.device
@@ -145,16 +164,17 @@ def paged_attention_decode(
     L = _lib.lib()
     ws = None
     ws_bytes = 0
+    sh = _stream_handle(stream, device)
     if num_seqs > 0:
         with torch.cuda.device(device):
             ws_bytes = L.pal_paged_attention_decode_workspace_size(
                 code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width, int(partition_size))
-        ws = _workspace(ws_bytes, device)
+        ws = _workspace(ws_bytes, device, sh)
     status = L.pal_paged_attention_decode(
         _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
         code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
         num_pages, width, int(partition_size),
-        _ptr(ws), ws_bytes, _stream_handle(stream, device),
+        _ptr(ws), ws.numel() if ws is not None else 0, sh,
     )
     _lib.check(status)
     return out
