@@ -89,11 +89,10 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
  * and the fp32 partials (max, exp-sum, unnormalised output) of KV segments
  * split between workers; its size follows from the number of wavefront
  * workers the device keeps resident.
- * partition_size: 0 (default: the KV blocks of the batch are shared out
- * evenly, three quarters statically and the rest in small chunks claimed by
- * whichever worker is free) or 128 / 256 / 512: fixed chunks of that many
- * tokens, each merged by log-sum-exp (the reference's CHUNK_SIZE is 512,
- * paged_attention_types.h:33).
+ * partition_size: 0 (default: the KV blocks of the batch are cut into one
+ * equal share per resident worker) or 128 / 256 / 512: fixed chunks of that
+ * many tokens, claimed by whichever worker is free and merged by log-sum-exp
+ * (the reference's CHUNK_SIZE is 512, paged_attention_types.h:33).
  * The workspace must be zero-filled before its first use; each call leaves
  * it ready for the next one on the same stream.
  */
@@ -125,6 +124,58 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                int tokens_per_page, int64_t num_pages, int64_t page_table_width,
                                int partition_size, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/*
+ * Replaces paged_attention_prefill (ops.py:87-130 -> bindings.cpp:74-124 ->
+ * ops.cpp:110-186 -> paged_attention_prefill_primitive.cpp:63-167).
+ * num_seqs = page-table rows; prompt_len P = num_query_rows / num_seqs
+ * (primitive :115-116); rows s*P .. s*P+P-1 of q_prompt / k_prompt /
+ * v_prompt ([rows, heads, head_dim]) are the prompt of sequence s, whose
+ * cached history is tokens [0, context_lens[s]) of its pages.  Prompt token
+ * i attends to the whole history plus prompt tokens 0..i, scale
+ * 1/sqrt(head_dim) (prefill.h.metal:147-234).  out: [num_query_rows *
+ * num_q_heads, head_dim], row (s*P + i) * num_q_heads + h; rows at and past
+ * num_seqs * P are not written.  head_dim % 32 == 0 (primitive :91-93).
+ * No workspace.
+ */
+int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, const void* v_prompt,
+                                const void* k_cache_paged, const void* v_cache_paged, const uint32_t* page_table,
+                                const int32_t* context_lens, void* out, int dtype, int64_t num_query_rows,
+                                int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* stream);
+
+/*
+ * Workspace bytes pal_paged_attention needs for num_query_rows rows on the
+ * current device (0 for unsupported arguments or without a device).  Zero-fill
+ * it before its first use; each call leaves it ready for the next one.
+ */
+size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, int num_kv_heads,
+                                          int head_dim, int tokens_per_page);
+
+/*
+ * Fused mixed batch of decode and prefill rows in one call.  The reference
+ * has no such function: it only prepares query_to_seq_map and
+ * query_token_offset in a benchmark
+ * (benchmarks/.../batch_latency_vs_num_sequences.cpp:124-131); this is the
+ * build's definition.  Row r (queries [num_query_rows, num_q_heads,
+ * head_dim]) belongs to sequence s = query_to_seq_map[r] and attends to
+ * tokens [0, min(sequence_lengths[s], query_token_offset[r])) of s's pages;
+ * new tokens must already be in the pages (pal_fill_kv_pages).  A decode row
+ * has offset >= its length; prompt token at absolute position p has offset
+ * p + 1.  Rows with no visible token, or naming no sequence (s >= num_seqs),
+ * yield zeros.  out: [num_query_rows, num_q_heads, head_dim].  Runs of
+ * consecutive rows of one sequence go to MFMA prefill tiles, single rows to
+ * the split-K decode kernels; a device-side planner builds that work list,
+ * so the call never reads row metadata on the host.  The workspace (size
+ * from pal_paged_attention_workspace_size, 256-byte aligned, zero-filled
+ * before its first use) must not be shared by concurrent calls.
+ */
+int pal_paged_attention(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
+                        const int32_t* sequence_lengths, const uint32_t* query_to_seq_map,
+                        const int32_t* query_token_offset, void* out, int dtype, int64_t num_query_rows,
+                        int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page,
+                        int64_t num_pages, int64_t page_table_width, void* workspace, size_t workspace_bytes,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -303,7 +303,8 @@ def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offs
     Row r belongs to sequence s = q2seq[r] and attends to the keys
     [0, min(seq_lens[s], q_offset[r])) of s, all read from pages.  A decode
     row uses q_offset = seq_lens[s]; a prefill row at absolute position p uses
-    q_offset = p + 1.  Returns [R, Hq, HD] float32.
+    q_offset = p + 1.  Rows with no visible key, or whose q2seq names no
+    sequence, are zero.  Returns [R, Hq, HD] float32.
     """
     q = bits_to_f32(queries, dtype)
     kf, vf = _pools_f32(k_pool, v_pool, dtype)
@@ -313,6 +314,8 @@ def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offs
     offs = np.asarray(q_offset).astype(np.int64)
     out = np.zeros(q.shape, np.float32)
     for s in np.unique(seqs):
+        if s >= pt.shape[0]:  # names no sequence: nothing to attend to
+            continue
         rows = np.nonzero(seqs == s)[0]
         limits = np.minimum(lens[s], offs[rows])
         n = int(max(0, limits.max()))

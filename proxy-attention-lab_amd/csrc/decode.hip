@@ -33,6 +33,10 @@
 //    O^T = V^T * P^T; V is read as 8-byte runs of 4 tokens from the [HD][TPP]
 //    layout as its A operand.  In O^T the head is the lane, so the online
 //    softmax rescale is a per-lane multiply.
+//  * Item mode (the decode rows of the fused op): item i is query row
+//    item_rows[i] of sequence q2seq[row], seeing min(len, q_offset[row]) keys;
+//    the item count is read from device memory.  Plain decode: item i is
+//    query row i of sequence i.
 //  * A segment that lies wholly inside one virtual worker writes the
 //    normalised output directly.  Split segments leave fp32 partials
 //    (max, exp-sum, unnormalised O) in one of two slots per virtual worker,
@@ -57,11 +61,46 @@ constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each
 constexpr int64_t kStaticShareNum = PAL_DECODE_STATIC_SHARE;
 constexpr int64_t kStaticShareDen = 4;
 
-__device__ __forceinline__ int64_t seq_blocks(const DecodeParams& p, int64_t s, int tpp) {
+// Number of items: the host's bound, or the count a planner left on the device.
+__device__ __forceinline__ int64_t item_count(const DecodeParams& p) {
+  if (!p.num_items_dev) return p.num_seqs;
+  const int64_t n = *p.num_items_dev;
+  return n < 0 ? 0 : (n < p.num_seqs ? n : p.num_seqs);
+}
+
+struct Item {
+  int64_t row;  // query / output row
+  int64_t seq;  // page-table row
+  int64_t len;  // visible keys, clamped to [0, W * TPP]
+};
+
+__device__ __forceinline__ Item item_at(const DecodeParams& p, int64_t i, int tpp) {
+  Item it;
+  int64_t len;
+  if (p.item_rows) {
+    it.row = p.item_rows[i];
+    const uint32_t sq = p.q2seq[it.row];
+    if (sq < p.num_pt_rows) {
+      it.seq = sq;
+      len = p.seq_lens[sq];
+      const int64_t off = p.q_offset[it.row];
+      len = off < len ? off : len;
+    } else {  // no such sequence: nothing to attend to
+      it.seq = 0;
+      len = 0;
+    }
+  } else {
+    it.row = i;
+    it.seq = i;
+    len = p.seq_lens[i];
+  }
   const int64_t max_tokens = p.page_table_width * tpp;
-  int64_t len = p.seq_lens[s];
-  len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
-  return (len + 15) >> 4;
+  it.len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
+  return it;
+}
+
+__device__ __forceinline__ int64_t seq_blocks(const DecodeParams& p, int64_t s, int tpp) {
+  return (item_at(p, s, tpp).len + 15) >> 4;
 }
 
 // The fixed cut of the global block list into virtual workers.
@@ -118,24 +157,6 @@ __device__ __forceinline__ int64_t locate_seq(const int64_t* cum, int64_t num_se
   return lo;
 }
 
-// Block-wide inclusive scan of int64 values over `threads` threads.
-template <int kThreads>
-__device__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_sums) {
-  const int lane = lane_id();
-  const int wv = static_cast<int>(threadIdx.x) >> 6;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int64_t o = __shfl_up(v, off, kWave);
-    if (lane >= off) v += o;
-  }
-  if (lane == kWave - 1) wave_sums[wv] = v;
-  __syncthreads();
-  int64_t add = 0;
-  for (int i = 0; i < wv; ++i) add += wave_sums[i];
-  __syncthreads();
-  return v + add;
-}
-
 // Scan for batches larger than kInlinePlanSeqs: cum[s] = first global block of
 // sequence s (all of its segments), cum[S] = hdr[0] = T.
 template <int TPP>
@@ -145,19 +166,21 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
   const int tid = threadIdx.x;
   int64_t carry = 0;
-  for (int64_t base = 0; base < p.num_seqs; base += kPlanThreads) {
+  const int64_t n = item_count(p);
+  for (int64_t base = 0; base < n; base += kPlanThreads) {
     const int64_t s = base + tid;
-    const int64_t v = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
+    const int64_t v = s < n ? seq_blocks(p, s, TPP) * segs : 0;
     const int64_t inc = block_inclusive_scan<kPlanThreads>(v, wave_sums);
-    if (s < p.num_seqs) p.cum[s] = carry + inc - v;
+    if (s < n) p.cum[s] = carry + inc - v;
     if (tid == kPlanThreads - 1) carry_sh = inc;
     __syncthreads();
     carry += carry_sh;
     __syncthreads();
   }
   if (tid == 0) {
-    p.cum[p.num_seqs] = carry;
+    p.cum[n] = carry;
     p.hdr[0] = carry;
+    p.hdr[1] = n;
   }
 }
 
@@ -170,7 +193,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
 // Streams the blocks of virtual worker v (one wavefront).
 template <int DT, int HD, int TPP>
 __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched& sc, const int64_t* cum,
-                                              int64_t v) {
+                                              int64_t n_items, int64_t v) {
   constexpr bool kK32 = (HD % 32) == 0;  // QK k-step of 32 (else 16)
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
   constexpr int NT = HD / 16;            // output tiles of 16 dims
@@ -183,7 +206,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   const int64_t b0 = vstart(sc, v);
   int64_t remaining = vstart(sc, v + 1) - b0;
   if (remaining <= 0) return;
-  int64_t s = locate_seq(cum, p.num_seqs, b0);
+  int64_t s = locate_seq(cum, n_items, b0);
   int64_t r = b0 - cum[s];
 
   const int lane = lane_id();
@@ -192,12 +215,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   const int segs = p.num_kv_heads * p.head_chunks;
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;  // elements per (page, kv head)
   const int64_t page_stride = head_block * p.num_kv_heads;
-  const int64_t max_tokens = p.page_table_width * TPP;
   bool first = true;
 
   while (remaining > 0) {
-    int64_t len = p.seq_lens[s];
-    len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
+    const Item it = item_at(p, s, TPP);
+    const int64_t len = it.len;
     const int64_t nb = (len + 15) >> 4;
     if (nb == 0) {  // empty sequence: no blocks, move on
       ++s;
@@ -219,7 +241,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     {
       const bool hv = r16 < hg;
       const uint32_t qmask = hv ? 0xFFFFFFFFu : 0u;
-      const uint16_t* qrow = p.q + (s * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
+      const uint16_t* qrow = p.q + (it.row * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         if constexpr (kK32) {
@@ -232,7 +254,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 
     const uint16_t* kbase = p.k_pool + kvh * head_block;
     const uint16_t* vbase = p.v_pool + kvh * head_block;
-    const uint32_t* pt = p.page_table + s * p.page_table_width;
+    const uint32_t* pt = p.page_table + it.seq * p.page_table_width;
 
     float m_run = -INFINITY;  // running max (raw score units) of head r16
     float l_run = 0.f;        // this lane's share of the exp-sum of head r16
@@ -350,7 +372,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
     if (r16 < hg) {
-      const int64_t row = s * p.num_q_heads + qh_base + r16;
+      const int64_t row = it.row * p.num_q_heads + qh_base + r16;
       if (complete) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
@@ -387,7 +409,9 @@ void decode_stream_kernel(const DecodeParams p) {
   const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
   const int64_t* cum = p.cum;
   int64_t total = 0;
+  int64_t n_items = 0;
   if (lds_plan) {
+    n_items = item_count(p);
     // Every workgroup scans the (at most 1024) sequence lengths into LDS:
     // thread t owns sequences 4t .. 4t+3.
     constexpr int kPer = kInlinePlanSeqs / kGroupThreads;
@@ -398,7 +422,7 @@ void decode_stream_kernel(const DecodeParams p) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int64_t s = static_cast<int64_t>(tid) * kPer + k;
-      vals[k] = s < p.num_seqs ? seq_blocks(p, s, TPP) * segs : 0;
+      vals[k] = s < n_items ? seq_blocks(p, s, TPP) * segs : 0;
       tsum += vals[k];
     }
     const int64_t incl = block_inclusive_scan<kGroupThreads>(tsum, wave_sums);
@@ -406,30 +430,34 @@ void decode_stream_kernel(const DecodeParams p) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int64_t s = static_cast<int64_t>(tid) * kPer + k;
-      if (s < p.num_seqs) cum_lds[s] = c;
+      if (s < n_items) cum_lds[s] = c;
       c += vals[k];
     }
-    if (tid == kGroupThreads - 1) cum_lds[p.num_seqs] = incl;
+    if (tid == kGroupThreads - 1) cum_lds[n_items] = incl;
     __syncthreads();
-    total = cum_lds[p.num_seqs];
+    total = cum_lds[n_items];
     if (blockIdx.x == 0) {  // the merge kernel reads the scan from the workspace
-      for (int64_t s = tid; s <= p.num_seqs; s += kGroupThreads) p.cum[s] = cum_lds[s];
-      if (tid == 0) p.hdr[0] = total;
+      for (int64_t s = tid; s <= n_items; s += kGroupThreads) p.cum[s] = cum_lds[s];
+      if (tid == 0) {
+        p.hdr[0] = total;
+        p.hdr[1] = n_items;
+      }
     }
     cum = cum_lds;
   } else {
     total = p.hdr[0];
+    n_items = p.hdr[1];
   }
   if (total == 0) return;
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
   const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (w < sc.nws) process_range<DT, HD, TPP>(p, sc, cum, w);
+  if (w < sc.nws) process_range<DT, HD, TPP>(p, sc, cum, n_items, w);
   while (sc.nc > 0) {
     uint32_t k = 0;
     if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
     k = __builtin_amdgcn_readfirstlane(k);
     if (k >= sc.nc) break;
-    process_range<DT, HD, TPP>(p, sc, cum, sc.nws + k);
+    process_range<DT, HD, TPP>(p, sc, cum, n_items, sc.nws + k);
   }
 }
 
@@ -443,13 +471,15 @@ void decode_stream_kernel(const DecodeParams p) {
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (row >= p.num_seqs * p.num_q_heads) return;
-  const int64_t s = row / p.num_q_heads;
-  const int qh = static_cast<int>(row - s * p.num_q_heads);
+  const int64_t wrow = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
+  if (wrow >= item_count(p) * p.num_q_heads) return;
+  const int64_t s = wrow / p.num_q_heads;
+  const int qh = static_cast<int>(wrow - s * p.num_q_heads);
+  const Item it = item_at(p, s, TPP);
+  const int64_t row = it.row * p.num_q_heads + qh;  // output row
   const int lane = lane_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
-  const int64_t nb = seq_blocks(p, s, TPP);
+  const int64_t nb = (it.len + 15) >> 4;
   const int64_t total = p.hdr[0];
   const int64_t cum_s = p.cum[s];
   if (nb == 0) {

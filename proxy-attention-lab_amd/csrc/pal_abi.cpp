@@ -46,6 +46,12 @@ bool decode_head_dim_supported(int hd) {
   return hd == 32 || hd == 64 || hd == 80 || hd == 96 || hd == 128 || hd == 256;
 }
 
+bool prefill_head_dim_supported(int hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 128 || hd == 256; }
+
+float scale_log2_for(int head_dim) {
+  return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
+}
+
 bool decode_partition_ok(int partition_size) {
   return partition_size == 0 || partition_size == 128 || partition_size == 256 || partition_size == 512;
 }
@@ -97,6 +103,83 @@ int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seq
   if (vw > (1LL << 28)) return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] problem too large for one call");
   *resident = res;
   *virtual_workers = vw;
+  return PAL_OK;
+}
+
+// Fused-op workspace: row metadata from the work-list builder, then a decode
+// workspace sized for every row being a decode item.
+struct FusedLayout {
+  size_t counts, item_rows, tiles, decode;
+  DecodeLayout dec;
+  size_t total;
+};
+
+FusedLayout fused_layout(int64_t num_rows, int head_dim, int hg_max, int64_t virtual_workers) {
+  FusedLayout l;
+  size_t off = 0;
+  l.counts = off;
+  off += 256;
+  l.item_rows = off;
+  off += align256(static_cast<size_t>(num_rows) * sizeof(int32_t));
+  l.tiles = off;
+  off += align256(static_cast<size_t>(num_rows) * 3 * sizeof(int32_t));
+  l.decode = off;
+  l.dec = decode_layout(num_rows, head_dim, hg_max, virtual_workers);
+  off += l.dec.total;
+  l.total = off;
+  return l;
+}
+
+// Common decode parameter set-up (plain decode: item i = row i = sequence i).
+pal::DecodeParams decode_params(const void* queries, const void* k_pool, const void* v_pool,
+                                const uint32_t* page_table, const int32_t* sequence_lengths, void* out,
+                                char* ws, const DecodeLayout& lay, int64_t num_items, int64_t num_pages,
+                                int64_t page_table_width, int num_q_heads, int num_kv_heads, int head_dim,
+                                int resident, int partition_size) {
+  const int group = num_q_heads / num_kv_heads;
+  pal::DecodeParams p;
+  p.q = static_cast<const uint16_t*>(queries);
+  p.k_pool = static_cast<const uint16_t*>(k_pool);
+  p.v_pool = static_cast<const uint16_t*>(v_pool);
+  p.page_table = page_table;
+  p.seq_lens = sequence_lengths;
+  p.out = static_cast<uint16_t*>(out);
+  p.item_rows = nullptr;
+  p.q2seq = nullptr;
+  p.q_offset = nullptr;
+  p.num_items_dev = nullptr;
+  p.num_pt_rows = num_items;
+  p.hdr = reinterpret_cast<int64_t*>(ws + lay.hdr);
+  p.claim = reinterpret_cast<uint32_t*>(ws + lay.claim);
+  p.cum = reinterpret_cast<int64_t*>(ws + lay.cum);
+  p.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
+  p.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  p.num_seqs = num_items;
+  p.num_pages = num_pages;
+  p.page_table_width = page_table_width;
+  p.num_q_heads = num_q_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = group;
+  p.head_chunks = (group + 15) / 16;
+  p.hg_max = group < 16 ? group : 16;
+  p.num_workers = resident;
+  p.tokens_per_worker = partition_size;
+  p.scale_log2 = scale_log2_for(head_dim);
+  return p;
+}
+
+// Checks shared by every attention entry point; returns PAL_OK or an error.
+int check_attention_dims(const char* op, int dtype, int num_q_heads, int num_kv_heads, int head_dim,
+                         int tokens_per_page, int64_t num_pages, int64_t page_table_width) {
+  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] unsupported dtype code %d", op, dtype);
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 || num_pages < 0 ||
+      page_table_width < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative or zero dimension", op);
+  if (num_q_heads % num_kv_heads != 0)
+    return fail(PAL_ERR_RUNTIME, "num_q_heads must be divisible by num_kv_heads (%d %% %d != 0)", num_q_heads,
+                num_kv_heads);
+  if (tokens_per_page != 16 && tokens_per_page != 32)
+    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for tokens_per_page %d (supported: 16, 32)", op, tokens_per_page);
   return PAL_OK;
 }
 
@@ -216,7 +299,9 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] %lld query rows for %lld sequences",
                 static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs));
   if (num_seqs == 0) return ok();
-  if (!queries || !k_pool || !v_pool || !sequence_lengths || !out || (page_table_width > 0 && !page_table))
+  if (num_pages == 0) page_table_width = 0;  // no page to read: every sequence is empty
+  if (!queries || !sequence_lengths || !out || (num_pages > 0 && (!k_pool || !v_pool)) ||
+      (page_table_width > 0 && !page_table))
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] null pointer argument");
   if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(PAL_ERR_INVALID_ARGUMENT,
@@ -236,32 +321,184 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 256-byte aligned");
 
-  char* ws = static_cast<char*>(workspace);
-  pal::DecodeParams p;
-  p.q = static_cast<const uint16_t*>(queries);
-  p.k_pool = static_cast<const uint16_t*>(k_pool);
-  p.v_pool = static_cast<const uint16_t*>(v_pool);
-  p.page_table = page_table;
-  p.seq_lens = sequence_lengths;
+  const pal::DecodeParams p = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
+                                            static_cast<char*>(workspace), lay, num_seqs, num_pages,
+                                            page_table_width, num_q_heads, num_kv_heads, head_dim, resident,
+                                            partition_size);
+  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)),
+                    "paged_attention_decode");
+}
+
+int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, const void* v_prompt,
+                                const void* k_cache_paged, const void* v_cache_paged, const uint32_t* page_table,
+                                const int32_t* context_lens, void* out, int dtype, int64_t num_query_rows,
+                                int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* stream) {
+  const char* op = "paged_attention_prefill";
+  int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                                page_table_width);
+  if (st != PAL_OK) return st;
+  if (num_query_rows < 0 || num_seqs < 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative dimension", op);
+  if (head_dim % 32 != 0)
+    return fail(PAL_ERR_RUNTIME, "[%s] head_dim %d must be divisible by 32", op, head_dim);
+  if (!prefill_head_dim_supported(head_dim))
+    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for head_dim %d (supported: 32, 64, 96, 128, 256)", op, head_dim);
+  if (num_seqs == 0) return ok();
+  if (num_pages == 0) page_table_width = 0;  // no page to read: no history
+  const int64_t prompt_len = num_query_rows / num_seqs;
+  if (prompt_len == 0) return ok();
+  if (!q_prompt || !k_prompt || !v_prompt || !context_lens || !out ||
+      (num_pages > 0 && (!k_cache_paged || !v_cache_paged)) || (page_table_width > 0 && !page_table))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
+  if (!aligned16(q_prompt) || !aligned16(k_prompt) || !aligned16(v_prompt) || !aligned16(k_cache_paged) ||
+      !aligned16(v_cache_paged) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] inputs must be 16-byte aligned, out 8-byte aligned", op);
+  const int group = num_q_heads / num_kv_heads;
+  const int hg_max = group < 16 ? group : 16;
+  const int qt = pal::prefill_tokens_per_tile(group);
+  const int64_t tiles = num_seqs * ((prompt_len + qt - 1) / qt);
+  if (tiles > 0x7fffffffLL || prompt_len > 0x3fffffffLL || num_query_rows > 0x7fffffffLL)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
+  pal::PrefillParams p;
+  p.q = static_cast<const uint16_t*>(q_prompt);
   p.out = static_cast<uint16_t*>(out);
-  p.hdr = reinterpret_cast<int64_t*>(ws + lay.hdr);
-  p.claim = reinterpret_cast<uint32_t*>(ws + lay.claim);
-  p.cum = reinterpret_cast<int64_t*>(ws + lay.cum);
-  p.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
-  p.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  p.k_pool = static_cast<const uint16_t*>(k_cache_paged);
+  p.v_pool = static_cast<const uint16_t*>(v_cache_paged);
+  p.k_dense = static_cast<const uint16_t*>(k_prompt);
+  p.v_dense = static_cast<const uint16_t*>(v_prompt);
+  p.page_table = page_table;
+  p.seq_lens = context_lens;
+  p.q_offset = nullptr;
+  p.tiles = nullptr;
+  p.num_tiles_dev = nullptr;
   p.num_seqs = num_seqs;
   p.num_pages = num_pages;
   p.page_table_width = page_table_width;
+  p.num_tiles = static_cast<int>(tiles);
+  p.prompt_len = static_cast<int>(prompt_len);
   p.num_q_heads = num_q_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = group;
-  p.head_chunks = chunks;
+  p.head_chunks = (group + 15) / 16;
   p.hg_max = hg_max;
-  p.num_workers = resident;
-  p.tokens_per_worker = partition_size;
-  p.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
-  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)),
-                    "paged_attention_decode");
+  p.scale_log2 = scale_log2_for(head_dim);
+  return hip_status(pal::launch_prefill(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)), op);
+}
+
+size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, int num_kv_heads,
+                                          int head_dim, int tokens_per_page) {
+  if (!valid_dtype(dtype) || num_query_rows <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0 || !prefill_head_dim_supported(head_dim) ||
+      (tokens_per_page != 16 && tokens_per_page != 32) || num_query_rows > 0x7fffffffLL)
+    return 0;
+  const int group = num_q_heads / num_kv_heads;
+  int resident = 0;
+  int64_t vw = 0;
+  if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
+                     &resident, &vw) != PAL_OK)
+    return 0;
+  return fused_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
+}
+
+int pal_paged_attention(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
+                        const int32_t* sequence_lengths, const uint32_t* query_to_seq_map,
+                        const int32_t* query_token_offset, void* out, int dtype, int64_t num_query_rows,
+                        int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page,
+                        int64_t num_pages, int64_t page_table_width, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const char* op = "paged_attention";
+  int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                                page_table_width);
+  if (st != PAL_OK) return st;
+  if (num_query_rows < 0 || num_seqs < 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative dimension", op);
+  if (!prefill_head_dim_supported(head_dim))
+    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for head_dim %d (supported: 32, 64, 96, 128, 256)", op, head_dim);
+  if (num_query_rows > 0x7fffffffLL || num_seqs > 0x7fffffffLL)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
+  if (num_query_rows == 0) return ok();
+  if (num_pages == 0) page_table_width = 0;  // no page to read: every row is empty
+  if (!queries || !sequence_lengths || !query_to_seq_map || !query_token_offset || !out ||
+      (num_pages > 0 && (!k_pool || !v_pool)) || (page_table_width > 0 && !page_table))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
+  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] queries and pools must be 16-byte aligned, out 8-byte aligned", op);
+  const int group = num_q_heads / num_kv_heads;
+  const int hg_max = group < 16 ? group : 16;
+  const int chunks = (group + 15) / 16;
+  int resident = 0;
+  int64_t vw = 0;
+  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, &resident, &vw);
+  if (st != PAL_OK) return st;
+  const FusedLayout lay = fused_layout(num_query_rows, head_dim, hg_max, vw);
+  if (workspace == nullptr || workspace_bytes < lay.total)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace of %zu bytes needed, %zu given", op, lay.total,
+                workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace must be 256-byte aligned", op);
+  int groups = 0;
+  hipError_t err = pal::prefill_resident_groups(dtype, head_dim, tokens_per_page, &groups);
+  if (err != hipSuccess) return hip_status(err, op);
+
+  char* ws = static_cast<char*>(workspace);
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + lay.counts);
+  int32_t* item_rows = reinterpret_cast<int32_t*>(ws + lay.item_rows);
+  int32_t* tiles = reinterpret_cast<int32_t*>(ws + lay.tiles);
+
+  // 1. work list
+  pal::FusedPlanParams fp;
+  fp.q2seq = query_to_seq_map;
+  fp.item_rows = item_rows;
+  fp.tiles = tiles;
+  fp.counts = counts;
+  fp.num_rows = num_query_rows;
+  fp.tokens_per_tile = pal::prefill_tokens_per_tile(group);
+  err = pal::launch_fused_plan(fp, hs);
+  if (err != hipSuccess) return hip_status(err, op);
+
+  // 2. prefill tiles: a persistent grid walks the list (twice the resident
+  //    workgroups, so the uneven cost of causal tiles evens out)
+  pal::PrefillParams pp;
+  pp.q = static_cast<const uint16_t*>(queries);
+  pp.out = static_cast<uint16_t*>(out);
+  pp.k_pool = static_cast<const uint16_t*>(k_pool);
+  pp.v_pool = static_cast<const uint16_t*>(v_pool);
+  pp.k_dense = nullptr;
+  pp.v_dense = nullptr;
+  pp.page_table = page_table;
+  pp.seq_lens = sequence_lengths;
+  pp.q_offset = query_token_offset;
+  pp.tiles = tiles;
+  pp.num_tiles_dev = counts + 1;
+  pp.num_seqs = num_seqs;
+  pp.num_pages = num_pages;
+  pp.page_table_width = page_table_width;
+  const int64_t gy = static_cast<int64_t>(num_kv_heads) * chunks;
+  int64_t gx = (2LL * groups + gy - 1) / gy;
+  const int64_t max_tiles = (num_query_rows + 1) / 2;  // every tile row belongs to a run of >= 2 rows
+  if (gx > max_tiles) gx = max_tiles;
+  if (gx < 1) gx = 1;
+  pp.num_tiles = static_cast<int>(gx);
+  pp.prompt_len = 0;
+  pp.num_q_heads = num_q_heads;
+  pp.num_kv_heads = num_kv_heads;
+  pp.group = group;
+  pp.head_chunks = chunks;
+  pp.hg_max = hg_max;
+  pp.scale_log2 = scale_log2_for(head_dim);
+  err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, hs);
+  if (err != hipSuccess) return hip_status(err, op);
+
+  // 3. decode items
+  pal::DecodeParams dp = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
+                                       ws + lay.decode, lay.dec, num_query_rows, num_pages, page_table_width,
+                                       num_q_heads, num_kv_heads, head_dim, resident, 0);
+  dp.item_rows = item_rows;
+  dp.q2seq = query_to_seq_map;
+  dp.q_offset = query_token_offset;
+  dp.num_items_dev = counts;
+  dp.num_pt_rows = num_seqs;
+  return hip_status(pal::launch_decode(dp, dtype, head_dim, tokens_per_page, hs), op);
 }
 
 }  // extern "C"

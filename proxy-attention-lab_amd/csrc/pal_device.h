@@ -108,4 +108,22 @@ __device__ __forceinline__ u32x2 mask4(u32x2 v, bool k0, bool k1, bool k2, bool 
   return r;
 }
 
+// Block-wide inclusive scan of int64 values over kThreads threads.
+template <int kThreads>
+__device__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_sums) {
+  const int lane = lane_id();
+  const int wv = static_cast<int>(threadIdx.x) >> 6;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t o = __shfl_up(v, off, kWave);
+    if (lane >= off) v += o;
+  }
+  if (lane == kWave - 1) wave_sums[wv] = v;
+  __syncthreads();
+  int64_t add = 0;
+  for (int i = 0; i < wv; ++i) add += wave_sums[i];
+  __syncthreads();
+  return v + add;
+}
+
 }  // namespace pal

@@ -13,7 +13,9 @@ from proxy_attention_lab.layout import (
 )
 from proxy_attention_lab.ops import (
     fill_kv_pages,
+    paged_attention,
     paged_attention_decode,
+    paged_attention_prefill,
 )
 
 __version__ = "2025.06.4+gfx950"
@@ -24,5 +26,7 @@ __all__ = [
     "get_k_cache_stripe_size",
     "get_optimal_page_size",
     "get_v_cache_shape",
+    "paged_attention",
     "paged_attention_decode",
+    "paged_attention_prefill",
 ]

@@ -27,7 +27,9 @@ from .layout import dtype_code, get_k_cache_stripe_size  # noqa: F401  (re-expor
 __all__ = [
     "fill_kv_pages",
     "get_k_cache_stripe_size",
+    "paged_attention",
     "paged_attention_decode",
+    "paged_attention_prefill",
 ]
 
 
@@ -71,20 +73,21 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_WORKSPACES: dict[tuple[str, int, int], torch.Tensor] = {}
 
 
-def _workspace(nbytes: int, device: torch.device, stream_handle: int) -> torch.Tensor | None:
-    """Persistent, zero-initialised workspace per (device, stream).
+def _workspace(kind: str, nbytes: int, device: torch.device, stream_handle: int) -> torch.Tensor | None:
+    """Persistent, zero-initialised workspace per (operator, device, stream).
 
     The decode kernels keep a work-claim counter in it that must read zero
     when a call starts; every call leaves it zero again, so the buffer is
-    reused as is by the next call on the same stream (calls on one stream
-    never overlap).  A larger request replaces it with a new zeroed buffer.
+    reused as is by the next call of the same operator on the same stream
+    (calls on one stream never overlap).  A larger request replaces it with a
+    new zeroed buffer.
     """
     if nbytes <= 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
+    key = (kind, device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -92,6 +95,37 @@ def _workspace(nbytes: int, device: torch.device, stream_handle: int) -> torch.T
         torch.cuda.current_stream(device).synchronize()
         _WORKSPACES[key] = ws
     return ws
+
+
+def _pools(op: str, k_pool: torch.Tensor, v_pool: torch.Tensor, device: torch.device, dtype: torch.dtype):
+    """Validate the paged pools; return (num_pages, Hkv, HD, TPP)."""
+    for name, t in (("k_cache_pool", k_pool), ("v_cache_pool", v_pool)):
+        _require_device(name, t, device)
+    if v_pool.dim() != 4:
+        raise ValueError(f"[{op}] v_cache_pool must be 4D [pages, kv_heads, head_dim, tokens_per_page]")
+    if k_pool.dim() != 5:
+        raise ValueError(f"[{op}] k_cache_pool must be 5D [pages, kv_heads, head_dim/x, tokens_per_page, x]")
+    num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in v_pool.shape)
+    if k_pool.dtype != dtype or v_pool.dtype != dtype:
+        raise ValueError(f"[{op}] queries and pools must share one dtype")
+    expect_k = (num_pages, num_kv_heads, head_dim // 8, tpp, 8)
+    if tuple(k_pool.shape) != expect_k:
+        raise ValueError(f"[{op}] k_cache_pool shape {tuple(k_pool.shape)} != {expect_k}")
+    return num_pages, num_kv_heads, head_dim, tpp
+
+
+def _query_dims(op: str, queries: torch.Tensor, head_dim: int):
+    """(rows, Hq) of 3-D [N, Hq, HD] or 2-D [N, HD] (one head) queries."""
+    if queries.dim() == 3:
+        num_rows, num_q_heads, q_hd = (int(x) for x in queries.shape)
+    elif queries.dim() == 2:
+        num_rows, q_hd = (int(x) for x in queries.shape)
+        num_q_heads = 1
+    else:
+        raise ValueError(f"[{op}] queries must be 2D [N, HD] or 3D [N, Hq, HD]")
+    if q_hd != head_dim:
+        raise ValueError(f"[{op}] query head_dim {q_hd} != cache head_dim {head_dim}")
+    return num_rows, num_q_heads
 
 
 # ---------------------------------------------------------------------------
@@ -126,30 +160,12 @@ def paged_attention_decode(
     splits the KV stream into fixed chunks of that many tokens instead, merged
     by log-sum-exp as in the reference's two-pass mode.
     """
+    op = "paged_attention_decode"
     _require_device("queries", queries)
     device = queries.device
-    for name, t in (("k_cache_pool", k_cache_pool), ("v_cache_pool", v_cache_pool)):
-        _require_device(name, t, device)
-    if v_cache_pool.dim() != 4:
-        raise ValueError("[paged_attention_decode] v_cache_pool must be 4D [pages, kv_heads, head_dim, tokens_per_page]")
-    if k_cache_pool.dim() != 5:
-        raise ValueError("[paged_attention_decode] k_cache_pool must be 5D [pages, kv_heads, head_dim/x, tokens_per_page, x]")
-    num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in v_cache_pool.shape)
-    if queries.dim() == 3:
-        num_rows, num_q_heads, q_hd = (int(x) for x in queries.shape)
-    elif queries.dim() == 2:
-        num_rows, q_hd = (int(x) for x in queries.shape)
-        num_q_heads = 1
-    else:
-        raise ValueError("[paged_attention_decode] queries must be 2D [N, HD] or 3D [N, Hq, HD]")
-    if q_hd != head_dim:
-        raise ValueError(f"[paged_attention_decode] query head_dim {q_hd} != cache head_dim {head_dim}")
     code = dtype_code(queries.dtype)
-    if k_cache_pool.dtype != queries.dtype or v_cache_pool.dtype != queries.dtype:
-        raise ValueError("[paged_attention_decode] queries and pools must share one dtype")
-    expect_k = (num_pages, num_kv_heads, head_dim // 8, tpp, 8)
-    if tuple(k_cache_pool.shape) != expect_k:
-        raise ValueError(f"[paged_attention_decode] k_cache_pool shape {tuple(k_cache_pool.shape)} != {expect_k}")
+    num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_pool, v_cache_pool, device, queries.dtype)
+    num_rows, num_q_heads = _query_dims(op, queries, head_dim)
     if page_table.dim() != 2:
         raise ValueError("[paged_attention_decode] page_table must be 2D [num_seqs, max_pages_per_seq]")
     num_seqs, width = (int(x) for x in page_table.shape)
@@ -169,7 +185,7 @@ def paged_attention_decode(
         with torch.cuda.device(device):
             ws_bytes = L.pal_paged_attention_decode_workspace_size(
                 code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width, int(partition_size))
-        ws = _workspace(ws_bytes, device, sh)
+        ws = _workspace("decode", ws_bytes, device, sh)
     status = L.pal_paged_attention_decode(
         _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
         code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
@@ -250,3 +266,125 @@ def fill_kv_pages(
     )
     _lib.check(status)
     return global_key_pool, global_value_pool
+
+
+def paged_attention_prefill(
+    q_prompt: torch.Tensor,
+    k_prompt: torch.Tensor,
+    v_prompt: torch.Tensor,
+    k_cache_paged: torch.Tensor,
+    v_cache_paged: torch.Tensor,
+    page_table: torch.Tensor,
+    context_len_arr: torch.Tensor,
+    stream=None,
+) -> torch.Tensor:
+    """Causal prefill of a uniform prompt per sequence over a paged history.
+
+    Reference: ops.py:87-130 -> bindings.cpp:74-124 -> ops.cpp:110-186 ->
+    paged_attention_prefill_primitive.cpp:63-167 -> prefill.h.metal:28-389.
+
+    S = page_table.shape[0] sequences, prompt length P = N // S (primitive
+    :115-116).  q_prompt: [N, Hq, HD] (or [N, HD]); k_prompt / v_prompt:
+    [N, Hkv, HD], rows s*P .. s*P+P-1 holding the prompt of sequence s.
+    Prompt token i of sequence s attends to the cached tokens
+    [0, context_len_arr[s]) of its pages and to prompt tokens 0..i.
+    Returns [N * Hq, HD], row (s*P + i) * Hq + h; rows past S*P (when N is
+    not a multiple of S) are zero.  HD % 32 == 0.  The prompt's K/V need not
+    be in the pages.
+    """
+    op = "paged_attention_prefill"
+    _require_device("q_prompt", q_prompt)
+    device = q_prompt.device
+    code = dtype_code(q_prompt.dtype)
+    num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_paged, v_cache_paged, device, q_prompt.dtype)
+    num_rows, num_q_heads = _query_dims(op, q_prompt, head_dim)
+    for name, t in (("k_prompt", k_prompt), ("v_prompt", v_prompt)):
+        _require_device(name, t, device)
+        if t.dtype != q_prompt.dtype:
+            raise ValueError(f"[{op}] {name} must have the query dtype")
+        if tuple(t.shape) != (num_rows, num_kv_heads, head_dim):
+            raise ValueError(f"[{op}] {name} must be [{num_rows}, {num_kv_heads}, {head_dim}], got {tuple(t.shape)}")
+    if page_table.dim() != 2:
+        raise ValueError(f"[{op}] page_table must be 2D [num_seqs, max_pages_per_seq]")
+    num_seqs, width = (int(x) for x in page_table.shape)
+    pt = _index_tensor("page_table", page_table, device)
+    ctx = _index_tensor("context_len_arr", context_len_arr, device)
+    if ctx.numel() < num_seqs:
+        raise ValueError(f"[{op}] {ctx.numel()} context lengths for {num_seqs} sequences")
+    q = q_prompt.contiguous()
+    kd = k_prompt.contiguous()
+    vd = v_prompt.contiguous()
+    kp = k_cache_paged.contiguous()
+    vp = v_cache_paged.contiguous()
+    out = torch.empty((num_rows * num_q_heads, head_dim), dtype=q_prompt.dtype, device=device)
+    covered = num_seqs * (num_rows // num_seqs) if num_seqs > 0 else 0
+    sh = _stream_handle(stream, device)
+    if covered < num_rows:
+        with torch.cuda.stream(torch.cuda.ExternalStream(sh, device=device)):
+            out[covered * num_q_heads:].zero_()
+    status = _lib.lib().pal_paged_attention_prefill(
+        _ptr(q), _ptr(kd), _ptr(vd), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(ctx), _ptr(out),
+        code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width, sh,
+    )
+    _lib.check(status)
+    return out
+
+
+def paged_attention(
+    queries: torch.Tensor,
+    k_cache_pool: torch.Tensor,
+    v_cache_pool: torch.Tensor,
+    page_table: torch.Tensor,
+    sequence_lengths: torch.Tensor,
+    query_to_seq_map: torch.Tensor,
+    query_token_offset: torch.Tensor,
+    stream=None,
+) -> torch.Tensor:
+    """Fused mixed batch: decode rows and prefill rows in one call.
+
+    No reference function exists; the arguments are those the reference
+    benchmark prepares (batch_latency_vs_num_sequences.cpp:124-131).
+    queries: [R, Hq, HD] (or [R, HD]); query_to_seq_map: [R] (u32/i32);
+    query_token_offset: [R] int32.  Row r of sequence s = query_to_seq_map[r]
+    attends to tokens [0, min(sequence_lengths[s], query_token_offset[r]))
+    of s's pages: a decode row passes an offset >= the length, the prompt
+    token at absolute position p passes p + 1 (its K/V already written by
+    fill_kv_pages).  Returns [R, Hq, HD]; rows that see no token, or name no
+    sequence, are zero.  Runs of consecutive rows of one sequence run as MFMA
+    prefill tiles, single rows on the split-K decode path.
+    """
+    op = "paged_attention"
+    _require_device("queries", queries)
+    device = queries.device
+    code = dtype_code(queries.dtype)
+    num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_pool, v_cache_pool, device, queries.dtype)
+    num_rows, num_q_heads = _query_dims(op, queries, head_dim)
+    if page_table.dim() != 2:
+        raise ValueError(f"[{op}] page_table must be 2D [num_seqs, max_pages_per_seq]")
+    num_seqs, width = (int(x) for x in page_table.shape)
+    pt = _index_tensor("page_table", page_table, device)
+    lens = _index_tensor("sequence_lengths", sequence_lengths, device)
+    q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
+    off = _index_tensor("query_token_offset", query_token_offset, device)
+    if lens.numel() < num_seqs:
+        raise ValueError(f"[{op}] {lens.numel()} sequence lengths for {num_seqs} sequences")
+    if q2s.numel() != num_rows or off.numel() != num_rows:
+        raise ValueError(f"[{op}] query_to_seq_map and query_token_offset need one entry per query row ({num_rows})")
+    q = queries.contiguous()
+    kp = k_cache_pool.contiguous()
+    vp = v_cache_pool.contiguous()
+    out = torch.empty((num_rows, num_q_heads, head_dim), dtype=queries.dtype, device=device)
+    L = _lib.lib()
+    sh = _stream_handle(stream, device)
+    ws = None
+    if num_rows > 0:
+        with torch.cuda.device(device):
+            ws_bytes = L.pal_paged_attention_workspace_size(code, num_rows, num_q_heads, num_kv_heads, head_dim, tpp)
+        ws = _workspace("fused", ws_bytes, device, sh)
+    status = L.pal_paged_attention(
+        _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(q2s), _ptr(off), _ptr(out),
+        code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width,
+        _ptr(ws), ws.numel() if ws is not None else 0, sh,
+    )
+    _lib.check(status)
+    return out

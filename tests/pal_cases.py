@@ -11,6 +11,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 
 import numpy as np
+import torch
 
 from oracle import pal_oracle as orc
 
@@ -126,3 +127,86 @@ def assert_close(actual_f32: np.ndarray, expected_f32: np.ndarray, dtype: str, w
             f"{what}: {len(bad)} of {a.size} elements outside atol={tol['atol']} rtol={tol['rtol']}; "
             f"max |diff| {np.nanmax(diff):.4g}; first at {i}: got {a[i]!r}, want {e[i]!r}"
         )
+
+
+def sdpa_prefill_case(seed, batch, hist, plen, hq, hkv, hd, dtype):
+    """The reference's prefill equivalency construction (prefill/test_sdpa_equivalency.py:51-117):
+    one causal SDPA over history + prompt, then keep the prompt rows."""
+    rng = np.random.default_rng(seed)
+    total = hist + plen
+    q = orc.f32_to_bits(rng.standard_normal((batch, hq, total, hd)).astype(np.float32), dtype)
+    k = orc.f32_to_bits(rng.standard_normal((batch, hkv, total, hd)).astype(np.float32), dtype)
+    v = orc.f32_to_bits(rng.standard_normal((batch, hkv, total, hd)).astype(np.float32), dtype)
+    qf, kf, vf = (torch.from_numpy(orc.bits_to_f32(a, dtype)) for a in (q, k, v))
+    g = hq // hkv
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        qf, kf.repeat_interleave(g, 1), vf.repeat_interleave(g, 1), is_causal=True)[:, :, hist:, :]
+    ref = ref.permute(0, 2, 1, 3).reshape(batch * plen * hq, hd).numpy()
+    q_prompt = q[:, :, hist:, :].transpose(0, 2, 1, 3).reshape(batch * plen, hq, hd)
+    k_prompt = k[:, :, hist:, :].transpose(0, 2, 1, 3).reshape(batch * plen, hkv, hd)
+    v_prompt = v[:, :, hist:, :].transpose(0, 2, 1, 3).reshape(batch * plen, hkv, hd)
+    tpp = 16
+    npg = (hist + tpp - 1) // tpp
+    k_pool = np.zeros(orc.k_cache_shape(batch * npg + 2, hkv, hd, tpp, dtype), np.uint16)
+    v_pool = np.zeros(orc.v_cache_shape(batch * npg + 2, hkv, hd, tpp, dtype), np.uint16)
+    perm = rng.permutation(batch * npg + 2)
+    pt = np.zeros((batch, max(npg, 1)), np.uint32)
+    for b in range(batch):
+        pt[b, :npg] = perm[b * npg:(b + 1) * npg]
+        orc.scatter_contiguous(k[b, :, :hist, :].transpose(1, 0, 2), v[b, :, :hist, :].transpose(1, 0, 2),
+                               k_pool, v_pool, pt[b])
+    lens = np.full(batch, hist, np.int32)
+    return q_prompt, k_prompt, v_prompt, k_pool, v_pool, pt, lens, ref
+
+
+def make_prefill_case(seed: int, hist_lens, prompt_len: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                      tokens_per_page: int, dtype: str, **kw):
+    """Paged history of hist_lens[s] tokens per sequence plus a uniform dense
+    prompt (the reference prefill's inputs): (case, q_prompt, k_prompt, v_prompt)."""
+    case = make_paged_case(seed, hist_lens, num_q_heads, num_kv_heads, head_dim, tokens_per_page, dtype, **kw)
+    rng = np.random.default_rng(seed + 1000)
+    rows = case.num_seqs * prompt_len
+    q = randn_bits(rng, (rows, num_q_heads, head_dim), dtype)
+    k = randn_bits(rng, (rows, num_kv_heads, head_dim), dtype)
+    v = randn_bits(rng, (rows, num_kv_heads, head_dim), dtype)
+    return case, q, k, v
+
+
+@dataclass
+class FusedCase:
+    case: PagedCase
+    queries: np.ndarray   # uint16 [R, Hq, HD]
+    q2seq: np.ndarray     # uint32 [R]
+    q_offset: np.ndarray  # int32 [R]
+
+
+def make_fused_case(seed: int, decode_lens, chunks, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                    tokens_per_page: int, dtype: str, *, block: int = 64, extra_offset: bool = True,
+                    **kw) -> FusedCase:
+    """A mixed batch: one decode row per entry of decode_lens, and for each
+    (cached, new) in chunks the `new` prompt rows at positions cached ..
+    cached+new-1 (offset p + 1), all K/V already in the pages.  Sequences are
+    the decode ones first, then one per chunk.  Rows are shuffled in blocks
+    (each decode row is a block, each chunk is cut into blocks of `block`
+    rows), so decode and prefill rows interleave.  With extra_offset, some
+    decode rows pass offset len + 1 (clamped to len by the op), as the
+    reference benchmark's history + 1 does."""
+    rng = np.random.default_rng(seed)
+    lens = list(int(x) for x in decode_lens) + [int(c) + int(n) for c, n in chunks]
+    case = make_paged_case(seed, lens, num_q_heads, num_kv_heads, head_dim, tokens_per_page, dtype, **kw)
+    blocks = []
+    nd = len(decode_lens)
+    for s in range(nd):
+        off = lens[s] + (1 if extra_offset and rng.random() < 0.5 else 0)
+        blocks.append((np.array([s], np.uint32), np.array([off], np.int32)))
+    for j, (cached, new) in enumerate(chunks):
+        s = nd + j
+        pos = np.arange(int(cached), int(cached) + int(new), dtype=np.int32)
+        for b0 in range(0, len(pos), block):
+            pb = pos[b0:b0 + block]
+            blocks.append((np.full(len(pb), s, np.uint32), pb + 1))
+    order = rng.permutation(len(blocks))
+    q2seq = np.concatenate([blocks[i][0] for i in order]) if blocks else np.zeros(0, np.uint32)
+    q_off = np.concatenate([blocks[i][1] for i in order]) if blocks else np.zeros(0, np.int32)
+    q = randn_bits(rng, (len(q2seq), num_q_heads, head_dim), dtype)
+    return FusedCase(case, q, q2seq.astype(np.uint32), q_off.astype(np.int32))

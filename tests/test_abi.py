@@ -100,3 +100,59 @@ def test_ops_reject_host_tensors_and_bad_ranks():
         pal.fill_kv_pages(q, q, v, v, pt, lens, lens)
     with pytest.raises(ValueError, match="4D"):
         pal.fill_kv_pages(q, q, k, k, pt, lens, lens)
+
+
+def test_prefill_rejects_bad_arguments_without_launch():
+    lib = _lib.lib()
+    args = dict(dtype=1, rows=8, seqs=2, hq=8, hkv=2, hd=128, tpp=16, pages=8, width=4)
+
+    def call(**over):
+        a = {**args, **over}
+        return lib.pal_paged_attention_prefill(None, None, None, None, None, None, None, None, a["dtype"], a["rows"],
+                                               a["seqs"], a["hq"], a["hkv"], a["hd"], a["tpp"], a["pages"],
+                                               a["width"], None)
+
+    assert call(hq=6, hkv=4) == _lib.PAL_ERR_RUNTIME and "divisible" in _lib.last_error()
+    assert call(hd=80) == _lib.PAL_ERR_RUNTIME and "32" in _lib.last_error()  # prefill_primitive.cpp:91-93
+    assert call(hd=160) == _lib.PAL_ERR_RUNTIME  # no kernel
+    assert call(tpp=8) == _lib.PAL_ERR_RUNTIME
+    assert call(dtype=7) == _lib.PAL_ERR_INVALID_ARGUMENT
+    assert call() == _lib.PAL_ERR_INVALID_ARGUMENT and "null" in _lib.last_error()
+    assert call(seqs=0) == 0  # nothing to do
+    assert call(rows=1, seqs=2) == 0  # prompt length 0
+
+
+def test_fused_rejects_bad_arguments_without_launch():
+    lib = _lib.lib()
+    args = dict(dtype=0, rows=8, seqs=2, hq=8, hkv=2, hd=128, tpp=16, pages=8, width=4)
+
+    def call(**over):
+        a = {**args, **over}
+        return lib.pal_paged_attention(None, None, None, None, None, None, None, None, a["dtype"], a["rows"],
+                                       a["seqs"], a["hq"], a["hkv"], a["hd"], a["tpp"], a["pages"], a["width"],
+                                       None, 0, None)
+
+    assert call(hq=6, hkv=4) == _lib.PAL_ERR_RUNTIME
+    assert call(hd=80) == _lib.PAL_ERR_RUNTIME
+    assert call(tpp=64) == _lib.PAL_ERR_RUNTIME
+    assert call(dtype=3) == _lib.PAL_ERR_INVALID_ARGUMENT
+    assert call(rows=-1) == _lib.PAL_ERR_INVALID_ARGUMENT
+    assert call() == _lib.PAL_ERR_INVALID_ARGUMENT and "null" in _lib.last_error()
+    assert call(rows=0) == 0
+    assert lib.pal_paged_attention_workspace_size(1, 64, 30, 8, 128, 16) == 0  # Hq % Hkv
+    assert lib.pal_paged_attention_workspace_size(1, 64, 32, 8, 80, 16) == 0  # head_dim
+    assert lib.pal_paged_attention_workspace_size(1, 0, 32, 8, 128, 16) == 0  # no rows
+
+
+def test_new_ops_reject_host_tensors_and_shapes():
+    q = torch.zeros(4, 4, 64, dtype=torch.float16)
+    k = torch.zeros(3, 1, 8, 16, 8, dtype=torch.float16)
+    v = torch.zeros(3, 1, 64, 16, dtype=torch.float16)
+    kd = torch.zeros(4, 1, 64, dtype=torch.float16)
+    pt = torch.zeros(2, 1, dtype=torch.int32)
+    lens = torch.ones(2, dtype=torch.int32)
+    rows = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="HIP device"):
+        pal.paged_attention_prefill(q, kd, kd, k, v, pt, lens)
+    with pytest.raises(ValueError, match="HIP device"):
+        pal.paged_attention(q, k, v, pt, lens, rows, rows)

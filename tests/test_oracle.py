@@ -17,7 +17,7 @@ import torch
 
 import kat_cases
 from oracle import pal_oracle as orc
-from pal_cases import assert_close, make_paged_case
+from pal_cases import assert_close, make_paged_case, sdpa_prefill_case
 
 DTYPES = ["f16", "bf16"]
 
@@ -217,36 +217,6 @@ def test_prefill_known_answers(dtype):
         np.testing.assert_allclose(out, expected, atol=1e-2, rtol=1e-3, err_msg=name)
 
 
-def _prefill_case(seed, batch, hist, plen, hq, hkv, hd, dtype):
-    """The reference's prefill equivalency construction (prefill/test_sdpa_equivalency.py:51-117):
-    one causal SDPA over history + prompt, then keep the prompt rows."""
-    rng = np.random.default_rng(seed)
-    total = hist + plen
-    q = orc.f32_to_bits(rng.standard_normal((batch, hq, total, hd)).astype(np.float32), dtype)
-    k = orc.f32_to_bits(rng.standard_normal((batch, hkv, total, hd)).astype(np.float32), dtype)
-    v = orc.f32_to_bits(rng.standard_normal((batch, hkv, total, hd)).astype(np.float32), dtype)
-    qf, kf, vf = (torch.from_numpy(orc.bits_to_f32(a, dtype)) for a in (q, k, v))
-    g = hq // hkv
-    ref = torch.nn.functional.scaled_dot_product_attention(
-        qf, kf.repeat_interleave(g, 1), vf.repeat_interleave(g, 1), is_causal=True)[:, :, hist:, :]
-    ref = ref.permute(0, 2, 1, 3).reshape(batch * plen * hq, hd).numpy()
-    q_prompt = q[:, :, hist:, :].transpose(0, 2, 1, 3).reshape(batch * plen, hq, hd)
-    k_prompt = k[:, :, hist:, :].transpose(0, 2, 1, 3).reshape(batch * plen, hkv, hd)
-    v_prompt = v[:, :, hist:, :].transpose(0, 2, 1, 3).reshape(batch * plen, hkv, hd)
-    tpp = 16
-    npg = (hist + tpp - 1) // tpp
-    k_pool = np.zeros(orc.k_cache_shape(batch * npg + 2, hkv, hd, tpp, dtype), np.uint16)
-    v_pool = np.zeros(orc.v_cache_shape(batch * npg + 2, hkv, hd, tpp, dtype), np.uint16)
-    perm = rng.permutation(batch * npg + 2)
-    pt = np.zeros((batch, max(npg, 1)), np.uint32)
-    for b in range(batch):
-        pt[b, :npg] = perm[b * npg:(b + 1) * npg]
-        orc.scatter_contiguous(k[b, :, :hist, :].transpose(1, 0, 2), v[b, :, :hist, :].transpose(1, 0, 2),
-                               k_pool, v_pool, pt[b])
-    lens = np.full(batch, hist, np.int32)
-    return q_prompt, k_prompt, v_prompt, k_pool, v_pool, pt, lens, ref
-
-
 # prefill/test_sdpa_equivalency.py:18-27
 PREFILL_CONFIGS = [(1, 0, 16, (4, 4), 64), (1, 128, 16, (4, 4), 64), (2, 64, 32, (8, 2), 128),
                    (1, 256, 1, (32, 8), 128), (1, 0, 128, (32, 8), 128)]
@@ -255,7 +225,7 @@ PREFILL_CONFIGS = [(1, 0, 16, (4, 4), 64), (1, 128, 16, (4, 4), 64), (2, 64, 32,
 @pytest.mark.parametrize("cfg", PREFILL_CONFIGS)
 def test_prefill_matches_torch_sdpa(cfg):
     b, hist, plen, (hq, hkv), hd = cfg
-    qp, kp, vp, k_pool, v_pool, pt, lens, ref = _prefill_case(21, b, hist, plen, hq, hkv, hd, "bf16")
+    qp, kp, vp, k_pool, v_pool, pt, lens, ref = sdpa_prefill_case(21, b, hist, plen, hq, hkv, hd, "bf16")
     ours = orc.paged_attention_prefill(qp, kp, vp, k_pool, v_pool, pt, lens, "bf16")
     np.testing.assert_allclose(ours, ref, atol=3e-5, rtol=3e-5)
 
@@ -273,7 +243,7 @@ def test_fused_matches_decode_and_prefill():
     np.testing.assert_allclose(fused, dec, atol=1e-6)
     # prefill part: history 30, prompt 20 -> write the prompt into pages, run fused.
     hist, plen = 30, 20
-    qp, kp, vp, k_pool, v_pool, pt, lens, ref = _prefill_case(22, 1, hist, plen, hq, hkv, hd, dtype)
+    qp, kp, vp, k_pool, v_pool, pt, lens, ref = sdpa_prefill_case(22, 1, hist, plen, hq, hkv, hd, dtype)
     pre = orc.paged_attention_prefill(qp, kp, vp, k_pool, v_pool, pt, lens, dtype)
     npg = (hist + plen + tpp - 1) // tpp
     extra = npg - pt.shape[1]
