@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
 """Benchmark of the PAL paged-attention path on one MI355X.
 
-Default workload ("config 2"): Llama-3-8B-shaped
+Headline workload ("config 2"): Llama-3-8B-shaped
 bf16 decode -- 64 sequences with context lengths drawn U[512, 4096], 32 query
 heads / 8 KV heads, head_dim 128, 16-token pages, a randomly permuted page
 table over a pool sized to the tokens plus 10 % free pages, N(0,1) values.
 One step = fill_kv_pages of each sequence's newest token (64 tokens) followed
-by paged_attention_decode of the 64 queries.
+by paged_attention_decode of the 64 queries.  value = algorithmic HBM bytes
+of the step / step time (GB/s); the roofline object is the decode operator's
+(its algorithmic bytes / its average duration from HIP events).  Several
+independent copies of the workload are rotated so that consecutive steps
+never hit in the 256 MB last-level cache.
 
-Prints one JSON line: value = algorithmic HBM bytes of the step / step time
-(GB/s), plus tokens/s, the decode kernel's roofline fraction measured live
-with HIP events, and a CPU baseline (the numpy oracle on the host cores, on a
-bounded sample).  Several independent copies of the workload are rotated so
-that consecutive steps never hit in the 256 MB last-level cache.
+The other configs are reported beside it, each in its own object:
+  c3  long-context split-K decode (8 x U[32768, 131072] tokens, 1 % of key
+      rows x8, partition 512 + log-sum-exp merge, and the default split)
+  c4  chunked causal prefill: fill_kv_pages of the new chunks, then causal
+      attention of the new rows over cached + new (fused operator), TFLOP/s
+      over causal-valid pairs only
+  c5  fused mixed batch, fp16: 256 decode rows + 4 prefill chunks of 1024
+      rows, interleaved in shuffled row blocks, one operator call
+The CPU baseline is the numpy oracle on the host cores on a bounded sample
+of config 2.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5]
 """
 
 from __future__ import annotations
@@ -46,6 +55,49 @@ METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"] if (ROOT / "
 # ---------------------------------------------------------------------------
 
 
+def paged_pool(rng: np.random.Generator, g: torch.Generator, lens: np.ndarray, hkv: int, hd: int, tpp: int,
+               dtype: torch.dtype, device, free_frac: float = 0.1):
+    """Pools of N(0,1) values with room for `lens` tokens per sequence plus
+    free pages, and a randomly permuted page table (numpy int32 [S, W])."""
+    pages_per_seq = (lens.astype(np.int64) + tpp - 1) // tpp
+    used = int(pages_per_seq.sum())
+    num_pages = max(1, used + int(math.ceil(free_frac * used)))
+    perm = rng.permutation(num_pages).astype(np.int32)
+    pt = np.zeros((len(lens), max(1, int(pages_per_seq.max()))), np.int32)
+    cur = 0
+    for s, n in enumerate(pages_per_seq):
+        pt[s, :n] = perm[cur:cur + n]
+        cur += n
+    k_pool = torch.randn(pal.get_k_cache_shape(num_pages, hkv, hd, tpp, dtype), generator=g, device=device,
+                         dtype=torch.float32).to(dtype)
+    v_pool = torch.randn(pal.get_v_cache_shape(num_pages, hkv, hd, tpp, dtype), generator=g, device=device,
+                         dtype=torch.float32).to(dtype)
+    return k_pool, v_pool, pt
+
+
+def causal_flops(hq: int, hd: int, cached: np.ndarray, new: np.ndarray) -> float:
+    """4 * Hq * HD * (causal-valid query/key pairs): QK^T and PV, 2 flops per MAC."""
+    c = cached.astype(np.float64)
+    n = new.astype(np.float64)
+    return float(4.0 * hq * hd * np.sum(n * c + n * (n + 1) / 2))
+
+
+def time_op(fn, steps: int, warmup: int, stream) -> tuple[float, float]:
+    """(mean ms per call from HIP events on `stream`, wall ms per call)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return float(np.mean([a.elapsed_time(b) for a, b in evs])), wall
+
+
 class DecodeWorkload:
     """Config 2 (or a variant): pools, page table, queries and the fill step's inputs."""
 
@@ -53,25 +105,12 @@ class DecodeWorkload:
                  dtype=torch.bfloat16, device="cuda:0"):
         rng = np.random.default_rng(1000 + seed)
         lens = rng.integers(ctx_lo, ctx_hi + 1, size=num_seqs).astype(np.int32)
-        pages_per_seq = (lens + tpp - 1) // tpp
-        used = int(pages_per_seq.sum())
-        num_pages = used + int(math.ceil(0.1 * used))
-        perm = rng.permutation(num_pages).astype(np.int32)
-        width = int(pages_per_seq.max())
-        pt = np.zeros((num_seqs, width), np.int32)
-        cur = 0
-        for s, n in enumerate(pages_per_seq):
-            pt[s, :n] = perm[cur:cur + n]
-            cur += n
         g = torch.Generator(device=device)
         g.manual_seed(2000 + seed)
+        self.k_pool, self.v_pool, pt = paged_pool(rng, g, lens, hkv, hd, tpp, dtype, device)
         self.lens_np, self.pt_np = lens, pt
         self.num_seqs, self.hq, self.hkv, self.hd, self.tpp = num_seqs, hq, hkv, hd, tpp
         self.dtype = dtype
-        self.k_pool = torch.randn(pal.get_k_cache_shape(num_pages, hkv, hd, tpp, dtype), generator=g,
-                                  device=device, dtype=torch.float32).to(dtype)
-        self.v_pool = torch.randn(pal.get_v_cache_shape(num_pages, hkv, hd, tpp, dtype), generator=g,
-                                  device=device, dtype=torch.float32).to(dtype)
         self.page_table = torch.from_numpy(pt).to(device)
         self.seq_lens = torch.from_numpy(lens).to(device)
         self.queries = torch.randn((num_seqs, hq, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
@@ -98,6 +137,102 @@ class DecodeWorkload:
 
     def fill_bytes(self) -> int:
         return 2 * self.num_seqs * self.hkv * self.hd * 2 * 2  # K and V: read new rows + write pool slots
+
+
+def long_context_workload(device, seed: int = 3) -> DecodeWorkload:
+    """Config 3: 8 sequences x U[32768, 131072] tokens, 32/8 heads, HD 128,
+    bf16; 1 % of key rows (token positions, all heads) scaled x8."""
+    w = DecodeWorkload(seed, num_seqs=8, ctx_lo=32768, ctx_hi=131072, device=device)
+    rng = np.random.default_rng(3000 + seed)
+    pages, slots = [], []
+    for s, n in enumerate(w.lens_np):
+        pos = rng.choice(int(n), size=max(1, int(n) // 100), replace=False)
+        pages.append(w.pt_np[s, pos // w.tpp])
+        slots.append(pos % w.tpp)
+    pi = torch.from_numpy(np.concatenate(pages).astype(np.int64)).to(device)
+    si = torch.from_numpy(np.concatenate(slots).astype(np.int64)).to(device)
+    w.k_pool[pi, :, :, si, :] = w.k_pool[pi, :, :, si, :] * 8
+    return w
+
+
+class PrefillWorkload:
+    """Config 4: 16 sequences, new chunk U[512, 2048] on cached U[0, 2048],
+    32/8 heads, HD 128, bf16.  Step 1 writes the new K/V through
+    fill_kv_pages; step 2 runs causal attention of the new rows over cached +
+    new (the fused operator: each sequence's rows form one run of tiles)."""
+
+    def __init__(self, device, seed: int = 4, num_seqs=16, hq=32, hkv=8, hd=128, tpp=16, dtype=torch.bfloat16):
+        rng = np.random.default_rng(4000 + seed)
+        self.new = rng.integers(512, 2049, size=num_seqs).astype(np.int32)
+        self.cached = rng.integers(0, 2049, size=num_seqs).astype(np.int32)
+        lens = self.cached + self.new
+        g = torch.Generator(device=device)
+        g.manual_seed(5000 + seed)
+        self.k_pool, self.v_pool, pt = paged_pool(rng, g, lens, hkv, hd, tpp, dtype, device)
+        self.hq, self.hkv, self.hd = hq, hkv, hd
+        n = int(self.new.sum())
+        self.rows = n
+        self.page_table = torch.from_numpy(pt).to(device)
+        self.seq_lens = torch.from_numpy(lens).to(device)
+        pos = np.concatenate([np.arange(c, c + k) for c, k in zip(self.cached, self.new)]).astype(np.int32)
+        q2s = np.repeat(np.arange(num_seqs), self.new).astype(np.int32)
+        self.write_pos = torch.from_numpy(pos).to(device)
+        self.q2seq = torch.from_numpy(q2s).to(device)
+        self.q_offset = torch.from_numpy(pos + 1).to(device)
+        self.queries = torch.randn((n, hq, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+        self.new_k = torch.randn((n, hkv, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+        self.new_v = torch.randn((n, hkv, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+
+    def fill(self):
+        pal.fill_kv_pages(self.new_k, self.new_v, self.k_pool, self.v_pool, self.page_table, self.write_pos,
+                          self.q2seq)
+
+    def attend(self):
+        return pal.paged_attention(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens,
+                                   self.q2seq, self.q_offset)
+
+    def flops(self) -> float:
+        return causal_flops(self.hq, self.hd, self.cached, self.new)
+
+    def fill_bytes(self) -> int:
+        return 2 * self.rows * self.hkv * self.hd * 2 * 2
+
+
+class FusedWorkload:
+    """Config 5: 256 decode rows (ctx U[256, 8192]) + 4 prefill chunks of
+    1024 new rows on U[0, 4096] cached tokens, 64/8 heads, HD 128, fp16; rows
+    in shuffled blocks (each decode row one block, prefill chunks in blocks
+    of 128 rows), one paged_attention call."""
+
+    def __init__(self, device, seed: int = 5, hq=64, hkv=8, hd=128, tpp=16, dtype=torch.float16, block=128):
+        rng = np.random.default_rng(6000 + seed)
+        dec = rng.integers(256, 8193, size=256).astype(np.int32)
+        cached = rng.integers(0, 4097, size=4).astype(np.int32)
+        new = np.full(4, 1024, np.int32)
+        lens = np.concatenate([dec, cached + new]).astype(np.int32)
+        g = torch.Generator(device=device)
+        g.manual_seed(7000 + seed)
+        self.k_pool, self.v_pool, pt = paged_pool(rng, g, lens, hkv, hd, tpp, dtype, device)
+        blocks = [(np.array([s], np.int32), np.array([dec[s]], np.int32)) for s in range(256)]
+        for j in range(4):
+            pos = np.arange(cached[j], cached[j] + new[j], dtype=np.int32)
+            for b0 in range(0, len(pos), block):
+                blocks.append((np.full(len(pos[b0:b0 + block]), 256 + j, np.int32), pos[b0:b0 + block] + 1))
+        order = rng.permutation(len(blocks))
+        q2s = np.concatenate([blocks[i][0] for i in order])
+        off = np.concatenate([blocks[i][1] for i in order])
+        self.rows = len(q2s)
+        self.page_table = torch.from_numpy(pt).to(device)
+        self.seq_lens = torch.from_numpy(lens).to(device)
+        self.q2seq = torch.from_numpy(q2s).to(device)
+        self.q_offset = torch.from_numpy(off).to(device)
+        self.queries = torch.randn((self.rows, hq, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+        self.decode_bytes = int(dec.astype(np.int64).sum()) * 2 * hkv * hd * 2 + 2 * 256 * hq * hd * 2
+        self.prefill_flops = causal_flops(hq, hd, cached, new)
+
+    def attend(self):
+        return pal.paged_attention(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens,
+                                   self.q2seq, self.q_offset)
 
 
 # ---------------------------------------------------------------------------
@@ -164,6 +299,9 @@ def main() -> int:
     ap.add_argument("--partition", type=int, default=0, help="decode partition size (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--configs", default="c2,c3,c4,c5",
+                    help="comma list of workloads to run (c2 is the headline; c3/c4/c5 are reported beside it)")
+    ap.add_argument("--extra-steps", type=int, default=20, help="timed calls per extra config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the timed loop, run one device-to-device copy of this many MiB (a kernel of "
                          "known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE)")
@@ -186,6 +324,11 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    configs = {c.strip() for c in args.configs.split(",") if c.strip()}
+    if "c2" not in configs:
+        extra = run_extra(configs, dev, args)
+        print(json.dumps({"metric": METRIC, "configs": sorted(configs), **extra}), flush=True)
+        return 0
     works = [DecodeWorkload(seed=i) for i in range(max(1, args.rotate))]
     w0 = works[0]
     torch.cuda.synchronize()
@@ -241,7 +384,7 @@ def main() -> int:
                         "paged_attention_decode)",
             "num_seqs": w0.num_seqs, "ctx": "U[512,4096]", "num_q_heads": w0.hq, "num_kv_heads": w0.hkv,
             "head_dim": w0.hd, "tokens_per_page": w0.tpp, "rotated_copies": len(works),
-            "partition_size": args.partition or 512,
+            "partition_size": args.partition if args.partition else "0 (one equal share per resident worker)",
         },
         "tokens_per_s": round(w0.num_seqs / (ms_per_step * 1e-3), 1),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
@@ -257,10 +400,63 @@ def main() -> int:
             "avg_launch_ms": round(dec_ms, 5),
         },
     }
+    del works
+    torch.cuda.empty_cache()
+    result.update(run_extra(configs, dev, args))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w0, args.cpu_budget)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def run_extra(configs: set[str], dev, args) -> dict:
+    """Configs 3, 4 and 5, each timed with HIP events around its operator calls."""
+    out = {}
+    stream = torch.cuda.current_stream(dev)
+    steps, warm = max(1, args.extra_steps), 3
+    if "c3" in configs:
+        w = long_context_workload(dev)
+        nbytes = w.decode_bytes()
+        res = {"workload": "config 3: 8 x U[32768,131072] ctx, 32/8 heads, HD 128, bf16, 1% key rows x8",
+               "context_tokens": int(w.lens_np.sum()), "algorithmic_bytes": nbytes}
+        for part in (512, 0):
+            ms, _ = time_op(lambda: w.decode(part), steps, warm, stream)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[f"partition_{part}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        out["long_context_decode"] = res
+        del w
+        torch.cuda.empty_cache()
+    if "c4" in configs:
+        w = PrefillWorkload(dev)
+        fill_ms, _ = time_op(w.fill, steps, warm, stream)
+        att_ms, _ = time_op(w.attend, steps, warm, stream)
+        fl = w.flops()
+        tf = fl / (att_ms * 1e-3) / 1e12
+        out["prefill"] = {
+            "workload": "config 4: 16 seqs, new U[512,2048] on cached U[0,2048], 32/8 heads, HD 128, bf16; "
+                        "fill_kv_pages of the new chunks, then causal attention (paged_attention, tile path)",
+            "rows": w.rows, "causal_flops": fl,
+            "attention_ms": round(att_ms, 4), "TFLOP/s": round(tf, 1),
+            "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "fill_ms": round(fill_ms, 4), "fill_GB/s": round(w.fill_bytes() / (fill_ms * 1e-3) / 1e9, 1),
+            "step_ms": round(att_ms + fill_ms, 4),
+        }
+        del w
+        torch.cuda.empty_cache()
+    if "c5" in configs:
+        w = FusedWorkload(dev)
+        ms, _ = time_op(w.attend, steps, warm, stream)
+        t_roof_ms = (w.decode_bytes / (HBM_PEAK_GBS * 1e9) + w.prefill_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12)) * 1e3
+        out["fused"] = {
+            "workload": "config 5: 256 decode rows ctx U[256,8192] + 4 x 1024 prefill rows on U[0,4096] cached, "
+                        "64/8 heads, HD 128, fp16, shuffled row blocks, one paged_attention call",
+            "rows": w.rows, "decode_bytes": w.decode_bytes, "prefill_flops": w.prefill_flops,
+            "ms": round(ms, 4), "roofline_ms": round(t_roof_ms, 4), "frac_of_roofline": round(t_roof_ms / ms, 4),
+        }
+        del w
+        torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":
