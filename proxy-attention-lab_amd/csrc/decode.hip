@@ -33,10 +33,11 @@
 //    O^T = V^T * P^T; V is read as 8-byte runs of 4 tokens from the [HD][TPP]
 //    layout as its A operand.  In O^T the head is the lane, so the online
 //    softmax rescale is a per-lane multiply.
-//  * Item mode (the decode rows of the fused op): item i is query row
-//    item_rows[i] of sequence q2seq[row], seeing min(len, q_offset[row]) keys;
-//    the item count is read from device memory.  Plain decode: item i is
-//    query row i of sequence i.
+//  * Row mode (the decode rows of the fused op): item i is query row i of
+//    sequence q2seq[i], seeing min(len, q_offset[i]) keys, when the row is
+//    alone in its run of same-sequence rows; rows of longer runs belong to
+//    the prefill kernel and are skipped here.  Plain decode: item i is query
+//    row i of sequence i.
 //  * A segment that lies wholly inside one virtual worker writes the
 //    normalised output directly.  Split segments leave fp32 partials
 //    (max, exp-sum, unnormalised O) in one of two slots per virtual worker,
@@ -61,36 +62,31 @@ constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each
 constexpr int64_t kStaticShareNum = PAL_DECODE_STATIC_SHARE;
 constexpr int64_t kStaticShareDen = 4;
 
-// Number of items: the host's bound, or the count a planner left on the device.
-__device__ __forceinline__ int64_t item_count(const DecodeParams& p) {
-  if (!p.num_items_dev) return p.num_seqs;
-  const int64_t n = *p.num_items_dev;
-  return n < 0 ? 0 : (n < p.num_seqs ? n : p.num_seqs);
-}
-
 struct Item {
   int64_t row;  // query / output row
   int64_t seq;  // page-table row
   int64_t len;  // visible keys, clamped to [0, W * TPP]
+  bool skip;    // row mode: a row of a multi-row run (not ours to write)
 };
 
 __device__ __forceinline__ Item item_at(const DecodeParams& p, int64_t i, int tpp) {
   Item it;
   int64_t len;
-  if (p.item_rows) {
-    it.row = p.item_rows[i];
-    const uint32_t sq = p.q2seq[it.row];
-    if (sq < p.num_pt_rows) {
+  it.row = i;
+  it.skip = false;
+  if (p.q2seq) {
+    const uint32_t sq = p.q2seq[i];
+    it.skip = (i > 0 && p.q2seq[i - 1] == sq) || (i + 1 < p.num_seqs && p.q2seq[i + 1] == sq);
+    if (sq < p.num_pt_rows && !it.skip) {
       it.seq = sq;
       len = p.seq_lens[sq];
-      const int64_t off = p.q_offset[it.row];
+      const int64_t off = p.q_offset[i];
       len = off < len ? off : len;
-    } else {  // no such sequence: nothing to attend to
+    } else {  // no such sequence, or a prefill row: nothing to attend to here
       it.seq = 0;
       len = 0;
     }
   } else {
-    it.row = i;
     it.seq = i;
     len = p.seq_lens[i];
   }
@@ -166,7 +162,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
   const int tid = threadIdx.x;
   int64_t carry = 0;
-  const int64_t n = item_count(p);
+  const int64_t n = p.num_seqs;
   for (int64_t base = 0; base < n; base += kPlanThreads) {
     const int64_t s = base + tid;
     const int64_t v = s < n ? seq_blocks(p, s, TPP) * segs : 0;
@@ -180,7 +176,6 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   if (tid == 0) {
     p.cum[n] = carry;
     p.hdr[0] = carry;
-    p.hdr[1] = n;
   }
 }
 
@@ -409,9 +404,8 @@ void decode_stream_kernel(const DecodeParams p) {
   const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
   const int64_t* cum = p.cum;
   int64_t total = 0;
-  int64_t n_items = 0;
+  const int64_t n_items = p.num_seqs;
   if (lds_plan) {
-    n_items = item_count(p);
     // Every workgroup scans the (at most 1024) sequence lengths into LDS:
     // thread t owns sequences 4t .. 4t+3.
     constexpr int kPer = kInlinePlanSeqs / kGroupThreads;
@@ -438,15 +432,11 @@ void decode_stream_kernel(const DecodeParams p) {
     total = cum_lds[n_items];
     if (blockIdx.x == 0) {  // the merge kernel reads the scan from the workspace
       for (int64_t s = tid; s <= n_items; s += kGroupThreads) p.cum[s] = cum_lds[s];
-      if (tid == 0) {
-        p.hdr[0] = total;
-        p.hdr[1] = n_items;
-      }
+      if (tid == 0) p.hdr[0] = total;
     }
     cum = cum_lds;
   } else {
     total = p.hdr[0];
-    n_items = p.hdr[1];
   }
   if (total == 0) return;
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
@@ -472,10 +462,11 @@ template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
   const int64_t wrow = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (wrow >= item_count(p) * p.num_q_heads) return;
+  if (wrow >= p.num_seqs * p.num_q_heads) return;
   const int64_t s = wrow / p.num_q_heads;
   const int qh = static_cast<int>(wrow - s * p.num_q_heads);
   const Item it = item_at(p, s, TPP);
+  if (it.skip) return;
   const int64_t row = it.row * p.num_q_heads + qh;  // output row
   const int lane = lane_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;

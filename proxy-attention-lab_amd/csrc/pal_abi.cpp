@@ -106,30 +106,6 @@ int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seq
   return PAL_OK;
 }
 
-// Fused-op workspace: row metadata from the work-list builder, then a decode
-// workspace sized for every row being a decode item.
-struct FusedLayout {
-  size_t counts, item_rows, tiles, decode;
-  DecodeLayout dec;
-  size_t total;
-};
-
-FusedLayout fused_layout(int64_t num_rows, int head_dim, int hg_max, int64_t virtual_workers) {
-  FusedLayout l;
-  size_t off = 0;
-  l.counts = off;
-  off += 256;
-  l.item_rows = off;
-  off += align256(static_cast<size_t>(num_rows) * sizeof(int32_t));
-  l.tiles = off;
-  off += align256(static_cast<size_t>(num_rows) * 3 * sizeof(int32_t));
-  l.decode = off;
-  l.dec = decode_layout(num_rows, head_dim, hg_max, virtual_workers);
-  off += l.dec.total;
-  l.total = off;
-  return l;
-}
-
 // Common decode parameter set-up (plain decode: item i = row i = sequence i).
 pal::DecodeParams decode_params(const void* queries, const void* k_pool, const void* v_pool,
                                 const uint32_t* page_table, const int32_t* sequence_lengths, void* out,
@@ -144,10 +120,8 @@ pal::DecodeParams decode_params(const void* queries, const void* k_pool, const v
   p.page_table = page_table;
   p.seq_lens = sequence_lengths;
   p.out = static_cast<uint16_t*>(out);
-  p.item_rows = nullptr;
   p.q2seq = nullptr;
   p.q_offset = nullptr;
-  p.num_items_dev = nullptr;
   p.num_pt_rows = num_items;
   p.hdr = reinterpret_cast<int64_t*>(ws + lay.hdr);
   p.claim = reinterpret_cast<uint32_t*>(ws + lay.claim);
@@ -357,7 +331,7 @@ int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, cons
   const int hg_max = group < 16 ? group : 16;
   const int qt = pal::prefill_tokens_per_tile(group);
   const int64_t tiles = num_seqs * ((prompt_len + qt - 1) / qt);
-  if (tiles > 0x7fffffffLL || prompt_len > 0x3fffffffLL || num_query_rows > 0x7fffffffLL)
+  if (tiles * num_kv_heads * ((group + 15) / 16) > 0x7fffffffLL || num_query_rows > 0x7fffffffLL)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
   pal::PrefillParams p;
   p.q = static_cast<const uint16_t*>(q_prompt);
@@ -369,12 +343,12 @@ int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, cons
   p.page_table = page_table;
   p.seq_lens = context_lens;
   p.q_offset = nullptr;
-  p.tiles = nullptr;
-  p.num_tiles_dev = nullptr;
+  p.q2seq = nullptr;
+  p.num_rows = num_query_rows;
   p.num_seqs = num_seqs;
   p.num_pages = num_pages;
   p.page_table_width = page_table_width;
-  p.num_tiles = static_cast<int>(tiles);
+  p.num_units = static_cast<int>(tiles);
   p.prompt_len = static_cast<int>(prompt_len);
   p.num_q_heads = num_q_heads;
   p.num_kv_heads = num_kv_heads;
@@ -382,6 +356,7 @@ int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, cons
   p.head_chunks = (group + 15) / 16;
   p.hg_max = hg_max;
   p.scale_log2 = scale_log2_for(head_dim);
+  p.scale_inv_log2 = 1.f / p.scale_log2;
   return hip_status(pal::launch_prefill(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)), op);
 }
 
@@ -397,7 +372,7 @@ size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int
   if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
                      &resident, &vw) != PAL_OK)
     return 0;
-  return fused_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
+  return decode_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
 }
 
 int pal_paged_attention(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
@@ -429,35 +404,19 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   int64_t vw = 0;
   st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, &resident, &vw);
   if (st != PAL_OK) return st;
-  const FusedLayout lay = fused_layout(num_query_rows, head_dim, hg_max, vw);
+  const DecodeLayout lay = decode_layout(num_query_rows, head_dim, hg_max, vw);
   if (workspace == nullptr || workspace_bytes < lay.total)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace of %zu bytes needed, %zu given", op, lay.total,
                 workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace must be 256-byte aligned", op);
-  int groups = 0;
-  hipError_t err = pal::prefill_resident_groups(dtype, head_dim, tokens_per_page, &groups);
-  if (err != hipSuccess) return hip_status(err, op);
-
-  char* ws = static_cast<char*>(workspace);
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  int32_t* counts = reinterpret_cast<int32_t*>(ws + lay.counts);
-  int32_t* item_rows = reinterpret_cast<int32_t*>(ws + lay.item_rows);
-  int32_t* tiles = reinterpret_cast<int32_t*>(ws + lay.tiles);
+  const int qt = pal::prefill_tokens_per_tile(group);
+  const int64_t windows = (num_query_rows + qt - 1) / qt;
+  if (windows * num_kv_heads * chunks > 0x7fffffffLL)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
 
-  // 1. work list
-  pal::FusedPlanParams fp;
-  fp.q2seq = query_to_seq_map;
-  fp.item_rows = item_rows;
-  fp.tiles = tiles;
-  fp.counts = counts;
-  fp.num_rows = num_query_rows;
-  fp.tokens_per_tile = pal::prefill_tokens_per_tile(group);
-  err = pal::launch_fused_plan(fp, hs);
-  if (err != hipSuccess) return hip_status(err, op);
-
-  // 2. prefill tiles: a persistent grid walks the list (twice the resident
-  //    workgroups, so the uneven cost of causal tiles evens out)
+  // 1. runs of rows of one sequence: MFMA tiles over windows of rows
   pal::PrefillParams pp;
   pp.q = static_cast<const uint16_t*>(queries);
   pp.out = static_cast<uint16_t*>(out);
@@ -468,17 +427,12 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   pp.page_table = page_table;
   pp.seq_lens = sequence_lengths;
   pp.q_offset = query_token_offset;
-  pp.tiles = tiles;
-  pp.num_tiles_dev = counts + 1;
+  pp.q2seq = query_to_seq_map;
+  pp.num_rows = num_query_rows;
   pp.num_seqs = num_seqs;
   pp.num_pages = num_pages;
   pp.page_table_width = page_table_width;
-  const int64_t gy = static_cast<int64_t>(num_kv_heads) * chunks;
-  int64_t gx = (2LL * groups + gy - 1) / gy;
-  const int64_t max_tiles = (num_query_rows + 1) / 2;  // every tile row belongs to a run of >= 2 rows
-  if (gx > max_tiles) gx = max_tiles;
-  if (gx < 1) gx = 1;
-  pp.num_tiles = static_cast<int>(gx);
+  pp.num_units = static_cast<int>(windows);
   pp.prompt_len = 0;
   pp.num_q_heads = num_q_heads;
   pp.num_kv_heads = num_kv_heads;
@@ -486,17 +440,16 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   pp.head_chunks = chunks;
   pp.hg_max = hg_max;
   pp.scale_log2 = scale_log2_for(head_dim);
-  err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, hs);
+  pp.scale_inv_log2 = 1.f / pp.scale_log2;
+  hipError_t err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, hs);
   if (err != hipSuccess) return hip_status(err, op);
 
-  // 3. decode items
+  // 2. rows alone in their run: split-K decode
   pal::DecodeParams dp = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
-                                       ws + lay.decode, lay.dec, num_query_rows, num_pages, page_table_width,
-                                       num_q_heads, num_kv_heads, head_dim, resident, 0);
-  dp.item_rows = item_rows;
+                                       static_cast<char*>(workspace), lay, num_query_rows, num_pages,
+                                       page_table_width, num_q_heads, num_kv_heads, head_dim, resident, 0);
   dp.q2seq = query_to_seq_map;
   dp.q_offset = query_token_offset;
-  dp.num_items_dev = counts;
   dp.num_pt_rows = num_seqs;
   return hip_status(pal::launch_decode(dp, dtype, head_dim, tokens_per_page, hs), op);
 }

@@ -40,21 +40,21 @@ struct DecodeParams {
   const uint16_t* v_pool;      // [P, Hkv, HD, TPP]
   const uint32_t* page_table;  // [S, W]
   const int32_t* seq_lens;     // [S]
-  uint16_t* out;               // [S, Hq, HD] (item mode: [R, Hq, HD])
-  // item mode (all null for plain decode): item i is query row item_rows[i]
-  // of sequence q2seq[row] with min(seq_lens[seq], q_offset[row]) keys
-  const int32_t* item_rows;
+  uint16_t* out;               // [S, Hq, HD] (row mode: [R, Hq, HD])
+  // row mode (both null for plain decode): item i is query row i of
+  // sequence q2seq[i] with min(seq_lens[seq], q_offset[i]) keys, if row i is
+  // alone in its run of same-sequence rows; other rows are skipped (the
+  // prefill kernel owns them)
   const uint32_t* q2seq;
   const int32_t* q_offset;
-  const int32_t* num_items_dev;  // item count written by a planner (<= num_seqs)
-  int64_t num_pt_rows;           // page-table rows (sequences) in item mode
+  int64_t num_pt_rows;           // page-table rows (sequences) in row mode
   // workspace
-  int64_t* hdr;                // hdr[0] = total blocks T, hdr[1] = items
+  int64_t* hdr;                // hdr[0] = total blocks T
   uint32_t* claim;             // dynamic-chunk counter: 0 on entry, re-armed to 0 by the merge kernel
   int64_t* cum;                // [S + 1] first global block of each sequence
   float* part_ml;              // [virtual workers][2][hg_max][2] (max * log2e * scale, exp-sum)
   float* part_o;               // [virtual workers][2][hg_max][HD]  unnormalised O
-  int64_t num_seqs;       // items (item mode: an upper bound)
+  int64_t num_seqs;       // items (row mode: query rows)
   int64_t num_pages;
   int64_t page_table_width;
   int num_q_heads;
@@ -71,52 +71,39 @@ struct DecodeParams {
 hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, int* workers);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
 
-// Causal attention over query tiles (prefill rows), all keys paged, or --
-// uniform-prompt mode -- keys past each sequence's history read from dense
-// prompt K/V.
+// Causal attention over query tiles (prefill rows).  Uniform-prompt mode
+// (prompt_len > 0): the reference prefill, keys past each sequence's history
+// read from dense prompt K/V.  Window mode (prompt_len == 0): the fused op's
+// rows in windows of `tokens per tile`; runs of one sequence are tiles, all
+// keys from pages, and lone rows are left to the decode kernels.
 struct PrefillParams {
   const uint16_t* q;           // [R, Hq, HD]
   uint16_t* out;               // [R, Hq, HD]
   const uint16_t* k_pool;      // [P, Hkv, HD/8, TPP, 8]
   const uint16_t* v_pool;      // [P, Hkv, HD, TPP]
-  const uint16_t* k_dense;     // uniform-prompt mode: [S * prompt_len, Hkv, HD]
+  const uint16_t* k_dense;     // prompt mode: [S * prompt_len, Hkv, HD]
   const uint16_t* v_dense;
   const uint32_t* page_table;  // [S, W]
-  const int32_t* seq_lens;     // list mode: keys per sequence; prompt mode: history per sequence
-  const int32_t* q_offset;     // list mode: [R] keys visible to each row (before the seq_lens clamp)
-  const int32_t* tiles;        // list mode: [max tiles][3] {first row, rows, sequence}
-  const int32_t* num_tiles_dev;  // list mode: number of tiles in `tiles`
+  const int32_t* seq_lens;     // window mode: keys per sequence; prompt mode: history per sequence
+  const int32_t* q_offset;     // window mode: [R] keys visible to each row (before the seq_lens clamp)
+  const uint32_t* q2seq;       // window mode: [R] sequence of each row
+  int64_t num_rows;            // R
   int64_t num_seqs;            // page-table rows
   int64_t num_pages;
   int64_t page_table_width;
-  int num_tiles;    // prompt mode: S * ceil(prompt_len / tokens per tile); list mode: workgroups along x
+  int num_units;    // prompt mode: S * ceil(prompt_len / tokens per tile); window mode: ceil(R / tokens per tile)
   int prompt_len;   // > 0 selects uniform-prompt mode
   int num_q_heads;
   int num_kv_heads;
   int group;
   int head_chunks;
   int hg_max;
-  float scale_log2;
+  float scale_log2;      // log2(e) / sqrt(HD)
+  float scale_inv_log2;  // 1 / scale_log2
 };
 
-// Query tokens per prefill tile for a GQA group size.
+// Query tokens per prefill tile (and window) for a GQA group size.
 int prefill_tokens_per_tile(int group);
 hipError_t launch_prefill(const PrefillParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
-// Prefill workgroups the GPU keeps resident at once.
-hipError_t prefill_resident_groups(int dtype, int head_dim, int tokens_per_page, int* groups);
-
-// Work-list builder of the fused op: splits the query rows into decode items
-// (rows alone in their run of same-sequence rows) and prefill tiles (up to
-// tokens_per_tile consecutive rows of one sequence).  counts[0] = items,
-// counts[1] = tiles.
-struct FusedPlanParams {
-  const uint32_t* q2seq;  // [R]
-  int32_t* item_rows;     // [R]
-  int32_t* tiles;         // [R][3]
-  int32_t* counts;        // [2]
-  int64_t num_rows;
-  int tokens_per_tile;
-};
-hipError_t launch_fused_plan(const FusedPlanParams& p, hipStream_t stream);
 
 }  // namespace pal

@@ -14,7 +14,9 @@
 //    query tokens of one sequence times the (up to 16) query heads sharing a
 //    kv head, so one K/V tile in LDS serves the whole GQA group.
 //  * Per 32-key step the workgroup stages K (as [HD/8][32][8], the page's own
-//    striped layout) and V (as [HD][32 + pad]) in LDS, double buffered, then
+//    striped layout) and V (as [HD][32 + pad]) in LDS, double buffered, with
+//    the global loads of the next step held in registers during the compute
+//    (one barrier per step); then
 //    each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
 //    from LDS, B = Q^T held in registers) and O^T += V^T * P^T with the same
 //    instruction.  In the transposed products a lane owns one M-row, so the
@@ -24,11 +26,12 @@
 //    moved when a score exceeds it by more than 2^8, so O is rescaled rarely.
 //  * Causal skipping: the key loop stops at the tile's largest limit, and key
 //    steps below every row's limit skip the mask arithmetic.
-//  * Two ways to name the work: a device-built list of tiles (the fused op;
-//    a persistent grid walks it), or the reference prefill's uniform prompt
-//    (S sequences x P prompt rows; tiles are pure arithmetic).  In the second
-//    mode keys [0, hist[s]) come from pages and keys hist[s] + i from the
-//    dense prompt K/V rows s*P + i, as prefill.h.metal:147-234 reads them.
+//  * Two ways to name the work, both without a planning pass: the reference
+//    prefill's uniform prompt (S sequences x P prompt rows; tiles are pure
+//    arithmetic; keys [0, hist[s]) come from pages and keys hist[s] + i from
+//    the dense prompt K/V rows s*P + i, as prefill.h.metal:147-234 reads
+//    them), or windows of consecutive query rows (the fused op), each run of
+//    rows of one sequence in a window being a tile.
 #include "pal_device.h"
 
 namespace pal {
@@ -42,33 +45,40 @@ constexpr int kKeys = 32;              // keys per step
 constexpr int kVPad = 8;               // extra elements per V row in LDS (bank spread)
 constexpr float kLazyRescale = 8.f;    // log2 headroom before the running max moves
 
-template <int DT, int HD, int TPP>
-__device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, int kvh, int h0, uint16_t* k_lds_base,
-                                             uint16_t* v_lds_base, int* lim_lds) {
+// Global -> register staging of one 32-key step: K as HD/8 stripes x 32 keys
+// and V as HD rows x 4 groups of 8 keys, 16 bytes per load, spread over the
+// workgroup's 256 threads.
+template <int HD>
+struct StepRegs {
+  static constexpr int kLoads = (HD * 4 + kPfThreads - 1) / kPfThreads;  // K (and V) loads per thread
+  u32x4 k[kLoads];
+  u32x4 v[kLoads];
+  int v_valid[kLoads];  // keys of the V group below the tile's largest limit (masked at store time)
+};
+
+// One query tile: rows [row0, row0 + nrows) of sequence s (nrows <= tokens
+// per tile), query heads h0 .. h0+15 of kv head kvh.  `hist` >= 0 selects the
+// uniform-prompt mode (keys below hist from pages, the rest from the dense
+// prompt rows of sequence s); hist < 0: every key from pages.
+template <int DT, int HD, int TPP, bool PROMPT>
+__device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, int nrows, int64_t s, int kvh, int h0,
+                                             uint16_t* k_lds_base, uint16_t* v_lds_base, int* lim_lds) {
   static_assert(HD % 32 == 0, "prefill needs head_dim % 32 == 0");
   constexpr int KS = HD / 16;  // QK k-steps of 16
   constexpr int DT32 = HD / 32;  // O^T row tiles of 32 dims
   constexpr int kVRow = kKeys + kVPad;
-  constexpr int NB = HD <= 128 ? 2 : 1;  // LDS buffers (double buffering up to HD 128)
+  constexpr int NL = StepRegs<HD>::kLoads;
   auto k_lds = [&](int b) { return k_lds_base + b * HD * kKeys; };
   auto v_lds = [&](int b) { return v_lds_base + b * HD * kVRow; };
 
+  // tile coordinates are workgroup-uniform: keep them in scalar registers so
+  // page-table reads are scalar loads
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  nrows = __builtin_amdgcn_readfirstlane(nrows);
+  s = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(s)));
   const int hg = min(16, p.group - h0);  // heads of this chunk
   const int qt = kMRows / p.hg_max;      // tokens per tile (hg_max = min(group, 16))
-  int row0, nrows;
-  int64_t s;
-  int64_t hist = 0;  // uniform-prompt mode: keys below hist come from pages
-  if (p.prompt_len > 0) {
-    const int tps = (p.prompt_len + qt - 1) / qt;
-    s = tile / tps;
-    const int j = tile - static_cast<int>(s) * tps;
-    row0 = static_cast<int>(s) * p.prompt_len + j * qt;
-    nrows = min(qt, p.prompt_len - j * qt);
-  } else {
-    row0 = p.tiles[3 * tile + 0];
-    nrows = p.tiles[3 * tile + 1];
-    s = static_cast<uint32_t>(p.tiles[3 * tile + 2]);
-  }
+  constexpr bool prompt_mode = PROMPT;
   const bool seq_ok = s < p.num_seqs;  // a row naming no sequence attends to nothing
   if (!seq_ok) s = 0;
   const int tid = threadIdx.x;
@@ -78,8 +88,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
   const int half = lane >> 5;
 
   const int64_t max_tokens = p.page_table_width * TPP;
+  int64_t hist = 0;  // prompt mode: keys below hist come from pages
   int64_t slen;
-  if (p.prompt_len > 0) {
+  if (prompt_mode) {
     hist = p.seq_lens[s];
     hist = hist < 0 ? 0 : (hist > max_tokens ? max_tokens : hist);
     slen = hist + p.prompt_len;
@@ -95,7 +106,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
     const int hh = tid % p.hg_max;
     int lim = 0;
     if (t < nrows && t < qt && hh < hg) {
-      int64_t off = p.prompt_len > 0 ? hist + (row0 + t - s * p.prompt_len) + 1 : p.q_offset[row0 + t];
+      int64_t off = prompt_mode ? hist + (row0 + t - s * p.prompt_len) + 1 : p.q_offset[row0 + t];
       off = off < 0 ? 0 : off;
       lim = static_cast<int>(off < slen ? off : slen);
     }
@@ -111,6 +122,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
       min_lim = min(min_lim, lim_lds[i]);
     }
   }
+  max_lim = __builtin_amdgcn_readfirstlane(max_lim);
+  min_lim = __builtin_amdgcn_readfirstlane(min_lim);
   const int m_row = w * 32 + col;  // this lane's M-row
   const int my_t = m_row / p.hg_max;
   const int my_h = m_row % p.hg_max;
@@ -131,83 +144,137 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;
   const int64_t page_stride = head_block * p.num_kv_heads;
   const uint32_t* pt = p.page_table + s * p.page_table_width;
-
   const int64_t dense_row0 = s * p.prompt_len - hist;  // dense row of key token tok: dense_row0 + tok
   const int64_t dense_stride = static_cast<int64_t>(p.num_kv_heads) * HD;
 
-  // Cooperative load of keys [k0, k0+32) into LDS buffer `buf`; keys past the
-  // tile's largest limit get zeros (and their scores are masked).
-  auto stage = [&](int k0, int buf) {
-    uint16_t* kl = k_lds(buf);
-    uint16_t* vl = v_lds(buf);
-    // K: 32 keys x HD/8 stripes of 16 B; thread -> (stripe, key), keys fastest.
-    for (int i = tid; i < kKeys * (HD / 8); i += kPfThreads) {
-      const int j = i % kKeys;
-      const int c = i / kKeys;
-      const int tok = k0 + j;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (tok < max_lim) {
-        if (tok < hist || p.prompt_len == 0) {
-          const uint32_t pg = pt[tok / TPP];
-          const int64_t off = kvh * head_block + (static_cast<int64_t>(c) * TPP + tok % TPP) * 8;
-          if (pg < p.num_pages)
-            val = *reinterpret_cast<const u32x4*>(p.k_pool + static_cast<int64_t>(pg) * page_stride + off);
-        } else {
+  // Page ids of the (at most two) pages holding keys [k0, k0+32): k0 is a
+  // multiple of 32 and TPP of 16.  Loaded one pipeline stage before the K/V
+  // loads that use them, so those never wait on a fresh load.
+  auto load_pages = [&](int k0, uint32_t& pg0, uint32_t& pg1) {
+    pg0 = pg1 = 0xFFFFFFFFu;
+    if (p.page_table_width > 0) {
+      const int64_t last = p.page_table_width - 1;
+      const int64_t i0 = k0 / TPP;
+      const int64_t i1 = (k0 + 16) / TPP;
+      pg0 = pt[i0 < last ? i0 : last];
+      pg1 = pt[i1 < last ? i1 : last];
+    }
+  };
+
+  // A step moves 4*HD items of 16 bytes for K and as many for V; thread tid
+  // takes items tid + 256 j.  With TPP = 16 the items are ordered page-major
+  // (2*HD per page), and 2*HD is a multiple of 64, so every load instruction
+  // of a wavefront reads one page: its base address is scalar and the
+  // per-thread offset within the page never changes.
+  //   K item: stripe c, key kj (0..31) -> LDS [c][kj][8]
+  //   V item: row d, keys kg .. kg+7   -> LDS [d][kg .. kg+7]
+  auto k_item = [&](int i, int& c, int& kj) {
+    if (TPP == 16) {
+      const int rem = i % (2 * HD);
+      c = rem / 16;
+      kj = (i / (2 * HD)) * 16 + rem % 16;
+    } else {
+      c = i / kKeys;
+      kj = i % kKeys;
+    }
+  };
+  auto v_item = [&](int i, int& d, int& kg) {
+    if (TPP == 16) {
+      const int rem = i % (2 * HD);
+      d = rem / 2;
+      kg = (i / (2 * HD)) * 16 + (rem % 2) * 8;
+    } else {
+      d = i / 4;
+      kg = (i % 4) * 8;
+    }
+  };
+  // page of load j of this wavefront (0: first page of the step, 1: second)
+  auto load_page_sel = [&](int j) { return TPP == 16 ? (w * kWave + j * kPfThreads) / (2 * HD) : 0; };
+  const int64_t kv_head_off = kvh * head_block;
+
+  // Global loads of keys [k0, k0+32) into registers; keys past the tile's
+  // largest limit read as zeros (and their scores are masked).
+  auto load_step = [&](int k0, StepRegs<HD>& r, uint32_t pg0v, uint32_t pg1v) {
+    const uint32_t pg0 = __builtin_amdgcn_readfirstlane(pg0v);
+    const uint32_t pg1 = __builtin_amdgcn_readfirstlane(pg1v);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int i = tid + j * kPfThreads;
+      const uint32_t pg = load_page_sel(j) ? pg1 : pg0;
+      const bool pg_ok = pg < p.num_pages;
+      const uint16_t* kpage = p.k_pool + static_cast<int64_t>(pg_ok ? pg : 0) * page_stride + kv_head_off;
+      const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg_ok ? pg : 0) * page_stride + kv_head_off;
+      int c, kj, d, kg;
+      k_item(i, c, kj);
+      v_item(i, d, kg);
+      const bool item_ok = i < HD * 4;
+      // K
+      {
+        u32x4 val = {0u, 0u, 0u, 0u};
+        const int tok = k0 + kj;
+        if (!prompt_mode || tok < hist) {
+          if (item_ok && pg_ok && tok < max_lim)
+            val = *reinterpret_cast<const u32x4*>(kpage + (c * TPP + kj % TPP) * 8);
+        } else if (item_ok && tok < max_lim) {
           val = *reinterpret_cast<const u32x4*>(p.k_dense + (dense_row0 + tok) * dense_stride + kvh * HD + c * 8);
         }
+        r.k[j] = val;
       }
-      *reinterpret_cast<u32x4*>(kl + (c * kKeys + j) * 8) = val;
-    }
-    // V: HD rows x 32 keys; thread -> (row d, 8-key group), 16 B per load.
-    for (int i = tid; i < HD * (kKeys / 8); i += kPfThreads) {
-      const int grp = i % (kKeys / 8);
-      const int d = i / (kKeys / 8);
-      const int tok = k0 + grp * 8;  // 8 keys, all in one page (TPP % 8 == 0)
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (tok < max_lim) {
-        if (tok + 8 <= hist || p.prompt_len == 0) {
-          const uint32_t pg = pt[tok / TPP];
-          const int64_t off = kvh * head_block + static_cast<int64_t>(d) * TPP + tok % TPP;
-          if (pg < p.num_pages)
-            val = *reinterpret_cast<const u32x4*>(p.v_pool + static_cast<int64_t>(pg) * page_stride + off);
-        } else {
+      // V
+      {
+        u32x4 val = {0u, 0u, 0u, 0u};
+        const int tok = k0 + kg;
+        if (!prompt_mode || tok + 8 <= hist) {
+          if (item_ok && pg_ok && tok < max_lim)
+            val = *reinterpret_cast<const u32x4*>(vpage + d * TPP + kg % TPP);
+        } else if (item_ok && tok < max_lim) {
           // some of the 8 keys are prompt tokens (dense, strided by row)
-          uint16_t e16[8];
+          uint32_t e16[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int t2 = tok + e;
+            const bool pgd = t2 < hist;
+            const uint16_t* src = pgd ? vpage + d * TPP + (kg + e) % TPP
+                                      : p.v_dense + (dense_row0 + t2) * dense_stride + kvh * HD + d;
             uint16_t x = 0;
-            if (t2 < max_lim) {
-              if (t2 < hist) {
-                const uint32_t pg = pt[t2 / TPP];
-                const int64_t off = kvh * head_block + static_cast<int64_t>(d) * TPP + t2 % TPP;
-                if (pg < p.num_pages) x = p.v_pool[static_cast<int64_t>(pg) * page_stride + off];
-              } else {
-                x = p.v_dense[(dense_row0 + t2) * dense_stride + kvh * HD + d];
-              }
-            }
+            if (t2 < max_lim && (!pgd || pg_ok)) x = *src;
             e16[e] = x;
           }
-          val = {static_cast<uint32_t>(e16[0]) | (static_cast<uint32_t>(e16[1]) << 16),
-                 static_cast<uint32_t>(e16[2]) | (static_cast<uint32_t>(e16[3]) << 16),
-                 static_cast<uint32_t>(e16[4]) | (static_cast<uint32_t>(e16[5]) << 16),
-                 static_cast<uint32_t>(e16[6]) | (static_cast<uint32_t>(e16[7]) << 16)};
+          val = {e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16)};
         }
-        // keys past the largest limit may hold anything (NaN bits included)
-        const int valid = max_lim - tok;
+        // keys past the largest limit may hold anything (NaN bits included);
+        // they are zeroed when the registers go to LDS, so no wait here
+        r.v_valid[j] = max_lim - tok;
+        r.v[j] = val;
+      }
+    }
+  };
+  auto store_step = [&](const StepRegs<HD>& r, int buf) {
+    uint16_t* kl = k_lds(buf);
+    uint16_t* vl = v_lds(buf);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int i = tid + j * kPfThreads;
+      if (i < HD * 4) {
+        int c, kj, d, kg;
+        k_item(i, c, kj);
+        v_item(i, d, kg);
+        *reinterpret_cast<u32x4*>(kl + (c * kKeys + kj) * 8) = r.k[j];
+        u32x4 v = r.v[j];
+        const int valid = r.v_valid[j];
         if (valid < 8) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t keep = (2 * e < valid ? 0x0000FFFFu : 0u) | (2 * e + 1 < valid ? 0xFFFF0000u : 0u);
-            val[e] &= keep;
+            v[e] &= keep;
           }
         }
+        *reinterpret_cast<u32x4*>(vl + d * kVRow + kg) = v;
       }
-      *reinterpret_cast<u32x4*>(vl + d * kVRow + grp * 8) = val;
     }
   };
 
-  float m_run = -INFINITY;  // running max of this lane's M-row, log2 units
+  float m_run = -INFINITY;  // running max of this lane's M-row (raw score units)
   float l_run = 0.f;        // this lane's share of the exp-sum
   f32x16 o[DT32];
 #pragma unroll
@@ -215,13 +282,28 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[n][r] = 0.f;
 
+  // Pipeline: while step st is computed from LDS, the K/V loads of step st+1
+  // are in flight in registers and the page ids of step st+2 in two more;
+  // after the compute the registers go to the other LDS buffer, the loads of
+  // step st+2 and the page ids of step st+3 are issued, and one barrier ends
+  // the step.
   const int nsteps = (max_lim + kKeys - 1) / kKeys;
-  if (nsteps > 0) stage(0, 0);
+  StepRegs<HD> regs;
+  uint32_t pga = 0xFFFFFFFFu, pgb = 0xFFFFFFFFu;
+  if (nsteps > 0) {
+    load_pages(0, pga, pgb);
+    load_step(0, regs, pga, pgb);
+    store_step(regs, 0);
+    if (nsteps > 1) {
+      load_pages(kKeys, pga, pgb);
+      load_step(kKeys, regs, pga, pgb);
+      if (nsteps > 2) load_pages(2 * kKeys, pga, pgb);
+    }
+  }
+  __syncthreads();
   for (int st = 0; st < nsteps; ++st) {
-    const int buf = NB == 2 ? (st & 1) : 0;
+    const int buf = st & 1;
     const int k0 = st * kKeys;
-    __syncthreads();  // buffer `buf` is staged; the other one is free
-    if (NB == 2 && st + 1 < nsteps) stage(k0 + kKeys, buf ^ 1);
 
     // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d]
     f32x16 sacc;
@@ -233,34 +315,36 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
       const u32x4 ka = *reinterpret_cast<const u32x4*>(k_lds(buf) + (c * kKeys + col) * 8);
       sacc = Dt<DT>::mma32x32x16(ka, qv[kk], sacc);
     }
-    // lane holds keys k0 + 8 (r/4) + 4 half + r%4 of M-row col
-    float sv[16];
+    // lane holds keys k0 + 8 (r/4) + 4 half + r%4 of M-row col.  Scores stay
+    // raw (the scale is positive, so maxima commute with it); the exponent is
+    // one fma: s * scale_log2 - m * scale_log2.
     float bm = -INFINITY;
-    const bool need_mask = k0 + kKeys > min_lim;
+    if (k0 + kKeys > min_lim) {  // some key of this step is masked for some row
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-      float x = sacc[r] * p.scale_log2;
-      if (need_mask && key >= my_lim) x = -INFINITY;
-      sv[r] = x;
-      bm = fmaxf(bm, x);
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (key >= my_lim) sacc[r] = -INFINITY;
+      }
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[r]);
     bm = fmaxf(bm, shfl_xor(bm, 32));
-    if (__ballot(bm > m_run + kLazyRescale)) {
+    if (__ballot(bm > m_run + kLazyRescale * p.scale_inv_log2)) {
+      const bool grow = bm > m_run + kLazyRescale * p.scale_inv_log2;
       const float m_new = fmaxf(m_run, bm);
-      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      // rows whose max did not grow keep alpha = 1 via m_new == m_run
-      const float a = (bm > m_run + kLazyRescale) ? alpha : 1.f;
-      if (bm > m_run + kLazyRescale) m_run = m_new;
+      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * p.scale_log2);
+      // rows whose max did not grow by more than the headroom keep their scale
+      const float a = grow ? alpha : 1.f;
+      if (grow) m_run = m_new;
       l_run *= a;
 #pragma unroll
       for (int n = 0; n < DT32; ++n) o[n] *= a;
     }
-    const float mb = (m_run == -INFINITY) ? 0.f : m_run;
+    const float mb = (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
     float pe[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      pe[r] = __builtin_amdgcn_exp2f(sv[r] - mb);
+      pe[r] = __builtin_amdgcn_exp2f(fmaf(sacc[r], p.scale_log2, mb));
       l_run += pe[r];
     }
     // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk covers the
@@ -279,10 +363,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
         o[n] = Dt<DT>::mma32x32x16(va, pb, o[n]);
       }
     }
-    if (NB == 1 && st + 1 < nsteps) {
-      __syncthreads();  // everyone is done reading the single buffer
-      stage(k0 + kKeys, 0);
+    if (st + 1 < nsteps) {
+      store_step(regs, buf ^ 1);  // buffer buf^1 was last read in step st-1, before the last barrier
+      if (st + 2 < nsteps) {
+        load_step(k0 + 2 * kKeys, regs, pga, pgb);
+        if (st + 3 < nsteps) load_pages(k0 + 3 * kKeys, pga, pgb);
+      }
     }
+    __syncthreads();
   }
 
   // ---- normalise and write: lane holds O[M-row col][32n + 8(r/4) + 4 half + r%4]
@@ -304,26 +392,63 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int tile, i
   }
 }
 
-// grid.y = kv heads x head chunks; grid.x walks the tiles (uniform-prompt
-// mode: exactly one tile per workgroup; list mode: a persistent stride over
-// the device-built list, whose length is read from the workspace).
+// Rows [0, R) of the query batch alternate runs of one sequence.  Is row r
+// alone in its run (a decode row, served by the decode kernels)?
+__device__ __forceinline__ bool single_row(const uint32_t* q2seq, int64_t r, int64_t n) {
+  const uint32_t sq = q2seq[r];
+  return (r == 0 || q2seq[r - 1] != sq) && (r + 1 == n || q2seq[r + 1] != sq);
+}
+
+// 1-D grid, XCD-aware: block b serves head group g = b % G (G = kv heads x
+// head chunks) and work unit b / G, so consecutive blocks -- which the
+// dispatcher spreads over the 8 XCDs -- take different kv heads, and each kv
+// head's K/V stay in few L2s.
+//  * prompt mode: unit = (sequence, tile), the last tile of a sequence first
+//    (it has the most keys);
+//  * window mode (fused op): unit = window of `tokens per tile` rows; every
+//    run of rows of one sequence inside the window that is not a lone decode
+//    row is computed as a tile.
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillParams p) {
-  constexpr int NB = HD <= 128 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[NB * HD * kKeys];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[NB * HD * (kKeys + kVPad)];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * HD * kKeys];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * HD * (kKeys + kVPad)];
   __shared__ int lim_lds[kMRows];
-  const int kvh = blockIdx.y / p.head_chunks;
-  const int h0 = (blockIdx.y % p.head_chunks) * 16;
-  const int n_tiles = p.prompt_len > 0 ? p.num_tiles : *p.num_tiles_dev;
-  for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x)
-    prefill_tile<DT, HD, TPP>(p, tile, kvh, h0, k_lds, v_lds, lim_lds);
+  __shared__ int run_start[kMRows];
+  const int G = p.num_kv_heads * p.head_chunks;
+  const int g = static_cast<int>(blockIdx.x % static_cast<unsigned>(G));
+  const int unit = static_cast<int>(blockIdx.x / static_cast<unsigned>(G));
+  const int kvh = g / p.head_chunks;
+  const int h0 = (g % p.head_chunks) * 16;
+  const int qt = kMRows / p.hg_max;
+  if (p.prompt_len > 0) {
+    const int tps = (p.prompt_len + qt - 1) / qt;
+    const int s = unit / tps;
+    const int j = tps - 1 - (unit - s * tps);
+    const int row0 = s * p.prompt_len + j * qt;
+    prefill_tile<DT, HD, TPP, true>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, lim_lds);
+    return;
+  }
+  const int w0 = unit * qt;
+  const int w1 = static_cast<int>(min(static_cast<int64_t>(w0 + qt), p.num_rows));
+  const int tid = threadIdx.x;
+  if (tid < w1 - w0) run_start[tid] = (tid == 0 || p.q2seq[w0 + tid] != p.q2seq[w0 + tid - 1]) ? 1 : 0;
+  __syncthreads();
+  int cur = w0;
+  while (cur < w1) {
+    int end = cur + 1;
+    while (end < w1 && !run_start[end - w0]) ++end;
+    end = __builtin_amdgcn_readfirstlane(end);
+    if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
+      prefill_tile<DT, HD, TPP, false>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, lim_lds);
+    cur = end;
+  }
 }
 
 template <int DT, int HD, int TPP>
 hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.num_tiles), static_cast<unsigned>(p.num_kv_heads * p.head_chunks));
-  hipLaunchKernelGGL((prefill_tile_kernel<DT, HD, TPP>), grid, dim3(kPfThreads), 0, stream, p);
+  const int64_t blocks = static_cast<int64_t>(p.num_units) * p.num_kv_heads * p.head_chunks;
+  hipLaunchKernelGGL((prefill_tile_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(blocks)), dim3(kPfThreads), 0,
+                     stream, p);
   return hipGetLastError();
 }
 
@@ -348,44 +473,12 @@ hipError_t prefill_hd(const PrefillParams& p, int hd, int tpp, hipStream_t strea
   }
 }
 
-template <int DT>
-const void* prefill_kernel_for(int hd, int tpp) {
-  const bool t32 = tpp == 32;
-  switch (hd) {
-    case 32: return t32 ? (const void*)&prefill_tile_kernel<DT, 32, 32> : (const void*)&prefill_tile_kernel<DT, 32, 16>;
-    case 64: return t32 ? (const void*)&prefill_tile_kernel<DT, 64, 32> : (const void*)&prefill_tile_kernel<DT, 64, 16>;
-    case 96: return t32 ? (const void*)&prefill_tile_kernel<DT, 96, 32> : (const void*)&prefill_tile_kernel<DT, 96, 16>;
-    case 128:
-      return t32 ? (const void*)&prefill_tile_kernel<DT, 128, 32> : (const void*)&prefill_tile_kernel<DT, 128, 16>;
-    case 256:
-      return t32 ? (const void*)&prefill_tile_kernel<DT, 256, 32> : (const void*)&prefill_tile_kernel<DT, 256, 16>;
-    default: return nullptr;
-  }
-}
-
 }  // namespace
-
-hipError_t prefill_resident_groups(int dtype, int head_dim, int tokens_per_page, int* groups) {
-  int dev = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return err;
-  int cus = 0;
-  err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (err != hipSuccess) return err;
-  const void* fn = dtype == kBF16 ? prefill_kernel_for<kBF16>(head_dim, tokens_per_page)
-                                  : prefill_kernel_for<kF16>(head_dim, tokens_per_page);
-  if (!fn) return hipErrorInvalidValue;
-  int per_cu = 0;
-  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPfThreads, 0);
-  if (err != hipSuccess) return err;
-  *groups = cus * (per_cu < 1 ? 1 : per_cu);
-  return hipSuccess;
-}
 
 int prefill_tokens_per_tile(int group) { return kMRows / (group < 16 ? group : 16); }
 
 hipError_t launch_prefill(const PrefillParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream) {
-  if (p.num_tiles <= 0) return hipSuccess;
+  if (p.num_units <= 0) return hipSuccess;
   if (dtype == kBF16) return prefill_hd<kBF16>(p, head_dim, tokens_per_page, stream);
   return prefill_hd<kF16>(p, head_dim, tokens_per_page, stream);
 }
