@@ -22,6 +22,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
@@ -42,8 +45,9 @@ struct Dt<kBF16> {
   static __device__ __forceinline__ uint16_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
   }
+  // one v_cvt_pk_bf16_f32 (round to nearest even)
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(from_f32(lo)) | (static_cast<uint32_t>(from_f32(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
   }
   static __device__ __forceinline__ f32x4 mma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -67,8 +71,9 @@ struct Dt<kF16> {
   static __device__ __forceinline__ uint16_t from_f32(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
   }
+  // one v_cvt_pk_f16_f32 (round to nearest even)
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(from_f32(lo)) | (static_cast<uint32_t>(from_f32(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
   }
   static __device__ __forceinline__ f32x4 mma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
@@ -88,6 +93,16 @@ struct Dt<kF16> {
 // wave64 helpers
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// max / sum of v and its value in lane l ^ 32 (v_permlane32_swap: no LDS trip)
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Index of this thread's wavefront, forced into a scalar register so that
 // addresses derived from it stay uniform (scalar loads of page-table entries).

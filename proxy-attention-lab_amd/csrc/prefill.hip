@@ -14,7 +14,8 @@
 //    query tokens of one sequence times the (up to 16) query heads sharing a
 //    kv head, so one K/V tile in LDS serves the whole GQA group.
 //  * Per 32-key step the workgroup stages K (as [HD/8][32][8], the page's own
-//    striped layout) and V (as [HD][32 + pad]) in LDS, double buffered, with
+//    striped layout) and V (as [HD][32 + 4], rows of 72 bytes so the PV
+//    operand reads are free of bank conflicts) in LDS, double buffered, with
 //    the global loads of the next step held in registers during the compute
 //    (one barrier per step); then
 //    each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
@@ -42,37 +43,79 @@ constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kMRows = kPfWaves * 32;  // M-rows (token, head) per workgroup
 constexpr int kKeys = 32;              // keys per step
-constexpr int kVPad = 8;               // extra elements per V row in LDS (bank spread)
+constexpr int kNBuf = 4;               // LDS step buffers (read by stragglers, computed, two in flight)
+constexpr int kPidChunk = 512;         // page ids staged per chunk; two chunks live in LDS
 constexpr float kLazyRescale = 8.f;    // log2 headroom before the running max moves
 
-// Global -> register staging of one 32-key step: K as HD/8 stripes x 32 keys
-// and V as HD rows x 4 groups of 8 keys, 16 bytes per load, spread over the
-// workgroup's 256 threads.
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kLgkmZero = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0) only
+
+// A step moves 4*HD items of 16 bytes of K and as many of V.
 template <int HD>
-struct StepRegs {
-  static constexpr int kLoads = (HD * 4 + kPfThreads - 1) / kPfThreads;  // K (and V) loads per thread
-  u32x4 k[kLoads];
-  u32x4 v[kLoads];
-  int v_valid[kLoads];  // keys of the V group below the tile's largest limit (masked at store time)
+struct StepGeo {
+  static constexpr int kItems = 4 * HD;
+  static constexpr int kLoads = (kItems + kPfThreads - 1) / kPfThreads;  // per thread, per K (or V)
+};
+
+// Item <-> (page, offset) maps.  LDS holds each step's items in item order,
+// so one direct-to-LDS load per wavefront fills 1 KiB of consecutive slots
+// (lane l -> slot base + l).  With TPP 16 the items are page-major (2*HD per
+// page), which also makes each load instruction read a single page.
+//   K item i: stripe c, key t within the page half ph:     page offset (c*TPP + t) * 8
+//   V item i: row d, 8-key group g' = g ^ swz(d) of the row: page offset d*TPP + 8 g'
+// The V groups are swizzled by row so that the PV operand reads (8 rows x 16
+// bytes per 8-lane group) hit 32 distinct banks.
+template <int HD, int TPP>
+struct ItemMap {
+  static __device__ __forceinline__ int k_page_half(int i) { return TPP == 16 ? i / (2 * HD) : 0; }
+  static __device__ __forceinline__ int k_offset(int i) {  // element offset inside the (page, kv head) block
+    if (TPP == 16) {
+      const int rem = i % (2 * HD);
+      return ((rem / 16) * TPP + rem % 16) * 8;
+    }
+    return ((i / 32) * TPP + i % 32) * 8;
+  }
+  static __device__ __forceinline__ int v_swz(int d) { return TPP == 16 ? (d >> 2) & 1 : (d >> 1) & 3; }
+  // V item i: row d and the group g stored in its slot (key offset in the step)
+  static __device__ __forceinline__ void v_item(int i, int& d, int& key) {
+    if (TPP == 16) {
+      const int rem = i % (2 * HD);
+      d = rem / 2;
+      key = (i / (2 * HD)) * 16 + 8 * ((rem % 2) ^ v_swz(d));
+    } else {
+      d = i / 4;
+      key = 8 * ((i % 4) ^ v_swz(d));
+    }
+  }
+  // LDS slot of K (key kj of the step, stripe c)
+  static __device__ __forceinline__ int k_slot(int kj, int c) {
+    return TPP == 16 ? (kj / 16) * (2 * HD) + c * 16 + kj % 16 : c * 32 + kj;
+  }
+  // LDS slot holding V row d, keys kg .. kg+7 of the step (kg multiple of 8)
+  static __device__ __forceinline__ int v_slot(int d, int kg) {
+    return TPP == 16 ? (kg / 16) * (2 * HD) + d * 2 + (((kg / 8) % 2) ^ v_swz(d)) : d * 4 + ((kg / 8) ^ v_swz(d));
+  }
 };
 
 // One query tile: rows [row0, row0 + nrows) of sequence s (nrows <= tokens
-// per tile), query heads h0 .. h0+15 of kv head kvh.  `hist` >= 0 selects the
-// uniform-prompt mode (keys below hist from pages, the rest from the dense
-// prompt rows of sequence s); hist < 0: every key from pages.
+// per tile), query heads h0 .. h0+15 of kv head kvh.  PROMPT: the
+// uniform-prompt mode (keys below the history length from pages, the rest
+// from the dense prompt rows of sequence s); otherwise every key from pages.
 template <int DT, int HD, int TPP, bool PROMPT>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, int nrows, int64_t s, int kvh, int h0,
-                                             uint16_t* k_lds_base, uint16_t* v_lds_base, int* lim_lds) {
+                                             uint16_t* k_lds_base, uint16_t* v_lds_base, uint16_t* junk_lds,
+                                             uint32_t* pid_lds, int* lim_lds) {
   static_assert(HD % 32 == 0, "prefill needs head_dim % 32 == 0");
   constexpr int KS = HD / 16;  // QK k-steps of 16
   constexpr int DT32 = HD / 32;  // O^T row tiles of 32 dims
-  constexpr int kVRow = kKeys + kVPad;
-  constexpr int NL = StepRegs<HD>::kLoads;
-  auto k_lds = [&](int b) { return k_lds_base + b * HD * kKeys; };
-  auto v_lds = [&](int b) { return v_lds_base + b * HD * kVRow; };
+  constexpr int NI = StepGeo<HD>::kItems;
+  constexpr int NL = StepGeo<HD>::kLoads;
+  using IM = ItemMap<HD, TPP>;
+  auto k_lds = [&](int b) { return k_lds_base + b * NI * 8; };
+  auto v_lds = [&](int b) { return v_lds_base + b * NI * 8; };
 
-  // tile coordinates are workgroup-uniform: keep them in scalar registers so
-  // page-table reads are scalar loads
+  // tile coordinates are workgroup-uniform: keep them in scalar registers
   row0 = __builtin_amdgcn_readfirstlane(row0);
   nrows = __builtin_amdgcn_readfirstlane(nrows);
   s = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(s)));
@@ -100,7 +143,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   }
 
   // Row limits: M-row m = token * hg_max + head.
-  __syncthreads();  // the previous tile is done with lim_lds and the K/V buffers
+  __syncthreads();  // the previous tile is done with every LDS array
   if (tid < kMRows) {
     const int t = tid / p.hg_max;
     const int hh = tid % p.hg_max;
@@ -146,95 +189,109 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   const uint32_t* pt = p.page_table + s * p.page_table_width;
   const int64_t dense_row0 = s * p.prompt_len - hist;  // dense row of key token tok: dense_row0 + tok
   const int64_t dense_stride = static_cast<int64_t>(p.num_kv_heads) * HD;
-
-  // Page ids of the (at most two) pages holding keys [k0, k0+32): k0 is a
-  // multiple of 32 and TPP of 16.  Loaded one pipeline stage before the K/V
-  // loads that use them, so those never wait on a fresh load.
-  auto load_pages = [&](int k0, uint32_t& pg0, uint32_t& pg1) {
-    pg0 = pg1 = 0xFFFFFFFFu;
-    if (p.page_table_width > 0) {
-      const int64_t last = p.page_table_width - 1;
-      const int64_t i0 = k0 / TPP;
-      const int64_t i1 = (k0 + 16) / TPP;
-      pg0 = pt[i0 < last ? i0 : last];
-      pg1 = pt[i1 < last ? i1 : last];
-    }
-  };
-
-  // A step moves 4*HD items of 16 bytes for K and as many for V; thread tid
-  // takes items tid + 256 j.  With TPP = 16 the items are ordered page-major
-  // (2*HD per page), and 2*HD is a multiple of 64, so every load instruction
-  // of a wavefront reads one page: its base address is scalar and the
-  // per-thread offset within the page never changes.
-  //   K item: stripe c, key kj (0..31) -> LDS [c][kj][8]
-  //   V item: row d, keys kg .. kg+7   -> LDS [d][kg .. kg+7]
-  auto k_item = [&](int i, int& c, int& kj) {
-    if (TPP == 16) {
-      const int rem = i % (2 * HD);
-      c = rem / 16;
-      kj = (i / (2 * HD)) * 16 + rem % 16;
-    } else {
-      c = i / kKeys;
-      kj = i % kKeys;
-    }
-  };
-  auto v_item = [&](int i, int& d, int& kg) {
-    if (TPP == 16) {
-      const int rem = i % (2 * HD);
-      d = rem / 2;
-      kg = (i / (2 * HD)) * 16 + (rem % 2) * 8;
-    } else {
-      d = i / 4;
-      kg = (i % 4) * 8;
-    }
-  };
-  // page of load j of this wavefront (0: first page of the step, 1: second)
-  auto load_page_sel = [&](int j) { return TPP == 16 ? (w * kWave + j * kPfThreads) / (2 * HD) : 0; };
   const int64_t kv_head_off = kvh * head_block;
+  const int nsteps = (max_lim + kKeys - 1) / kKeys;
+  // page-table entries the tile reads: keys below max_lim, and in prompt mode
+  // only those below the history (the rest are dense) -- never past the width
+  const int paged_keys = prompt_mode ? min(max_lim, static_cast<int>(hist)) : max_lim;
+  const int n_pid = (paged_keys + TPP - 1) / TPP;
 
-  // Global loads of keys [k0, k0+32) into registers; keys past the tile's
-  // largest limit read as zeros (and their scores are masked).
-  auto load_step = [&](int k0, StepRegs<HD>& r, uint32_t pg0v, uint32_t pg1v) {
-    const uint32_t pg0 = __builtin_amdgcn_readfirstlane(pg0v);
-    const uint32_t pg1 = __builtin_amdgcn_readfirstlane(pg1v);
+  // Page ids live in LDS (two chunks of 512 entries, entry e in slot e % 1024):
+  // reading them is an LDS broadcast, so the only vector-memory traffic in the
+  // step loop is the K/V copies, whose count the waits below rely on.
+  auto stage_pids = [&](int chunk) {  // synchronous; callers hold a barrier after it
+    for (int e = chunk * kPidChunk + tid; e < min((chunk + 1) * kPidChunk, n_pid); e += kPfThreads)
+      pid_lds[e % (2 * kPidChunk)] = pt[e];
+  };
+  auto page_of = [&](int e) { return __builtin_amdgcn_readfirstlane(pid_lds[e % (2 * kPidChunk)]); };
+
+  // Fast step: all 32 keys below the tile's largest limit, in valid pages
+  // (and, in prompt mode, below the history): one direct-to-LDS copy per item,
+  // no registers, nothing to wait for here.  Every wavefront issues exactly
+  // 2*NL copies (items past the step go to a junk slot), so the wait counts
+  // are the same on every wavefront.
+  // Slow step (tile end, invalid pages, dense prompt keys): register loads,
+  // masked, then LDS stores -- synchronous, so it also drains the copies in
+  // flight, which keeps the counted waits safe.
+  auto issue = [&](int j) {
+    const int buf = j % kNBuf;
+    const int k0 = j * kKeys;
+    const uint32_t pg0 = page_of(k0 / TPP);
+    const uint32_t pg1 = TPP == 16 ? page_of(k0 / TPP + 1) : pg0;
+    const bool fast = k0 + kKeys <= max_lim && pg0 < p.num_pages && pg1 < p.num_pages &&
+                      (!prompt_mode || k0 + kKeys <= hist);
+    if (fast) {
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      const int i = tid + j * kPfThreads;
-      const uint32_t pg = load_page_sel(j) ? pg1 : pg0;
+      for (int jj = 0; jj < NL; ++jj) {
+        const int i = tid + jj * kPfThreads;
+        const int ib = w * kWave + jj * kPfThreads;  // first item of this wavefront's load
+        const bool ok = ib < NI;
+        const uint32_t pg = IM::k_page_half(ok ? ib : 0) ? pg1 : pg0;
+        const uint16_t* page = p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off;
+        const uint16_t* src = page + (ok ? IM::k_offset(i) : 0);
+        uint16_t* dst = ok ? k_lds(buf) + ib * 8 : junk_lds;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      }
+#pragma unroll
+      for (int jj = 0; jj < NL; ++jj) {
+        const int i = tid + jj * kPfThreads;
+        const int ib = w * kWave + jj * kPfThreads;
+        const bool ok = ib < NI;
+        const uint32_t pg = IM::k_page_half(ok ? ib : 0) ? pg1 : pg0;
+        const uint16_t* page = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off;
+        int d = 0, key = 0;
+        if (ok) IM::v_item(i, d, key);
+        const uint16_t* src = page + d * TPP + key % TPP;
+        uint16_t* dst = ok ? v_lds(buf) + ib * 8 : junk_lds;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      }
+      return;
+    }
+#pragma unroll
+    for (int jj = 0; jj < NL; ++jj) {
+      const int i = tid + jj * kPfThreads;
+      if (i >= NI) continue;
+      const uint32_t pg = IM::k_page_half(i) ? pg1 : pg0;
       const bool pg_ok = pg < p.num_pages;
-      const uint16_t* kpage = p.k_pool + static_cast<int64_t>(pg_ok ? pg : 0) * page_stride + kv_head_off;
-      const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg_ok ? pg : 0) * page_stride + kv_head_off;
-      int c, kj, d, kg;
-      k_item(i, c, kj);
-      v_item(i, d, kg);
-      const bool item_ok = i < HD * 4;
-      // K
+      // K: stripe c, key kj of the step
       {
-        u32x4 val = {0u, 0u, 0u, 0u};
+        int kj, c;
+        if (TPP == 16) {
+          const int rem = i % (2 * HD);
+          c = rem / 16;
+          kj = (i / (2 * HD)) * 16 + rem % 16;
+        } else {
+          c = i / 32;
+          kj = i % 32;
+        }
         const int tok = k0 + kj;
+        u32x4 val = {0u, 0u, 0u, 0u};
         if (!prompt_mode || tok < hist) {
-          if (item_ok && pg_ok && tok < max_lim)
-            val = *reinterpret_cast<const u32x4*>(kpage + (c * TPP + kj % TPP) * 8);
-        } else if (item_ok && tok < max_lim) {
+          if (pg_ok && tok < max_lim)
+            val = *reinterpret_cast<const u32x4*>(p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off +
+                                                  IM::k_offset(i));
+        } else if (tok < max_lim) {
           val = *reinterpret_cast<const u32x4*>(p.k_dense + (dense_row0 + tok) * dense_stride + kvh * HD + c * 8);
         }
-        r.k[j] = val;
+        *reinterpret_cast<u32x4*>(k_lds(buf) + i * 8) = val;
       }
-      // V
+      // V: row d, keys key .. key+7 of the step
       {
+        int d, key;
+        IM::v_item(i, d, key);
+        const int tok = k0 + key;
+        const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off + d * TPP;
         u32x4 val = {0u, 0u, 0u, 0u};
-        const int tok = k0 + kg;
         if (!prompt_mode || tok + 8 <= hist) {
-          if (item_ok && pg_ok && tok < max_lim)
-            val = *reinterpret_cast<const u32x4*>(vpage + d * TPP + kg % TPP);
-        } else if (item_ok && tok < max_lim) {
+          if (pg_ok && tok < max_lim) val = *reinterpret_cast<const u32x4*>(vpage + key % TPP);
+        } else if (tok < max_lim) {
           // some of the 8 keys are prompt tokens (dense, strided by row)
           uint32_t e16[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int t2 = tok + e;
             const bool pgd = t2 < hist;
-            const uint16_t* src = pgd ? vpage + d * TPP + (kg + e) % TPP
+            const uint16_t* src = pgd ? vpage + (key + e) % TPP
                                       : p.v_dense + (dense_row0 + t2) * dense_stride + kvh * HD + d;
             uint16_t x = 0;
             if (t2 < max_lim && (!pgd || pg_ok)) x = *src;
@@ -242,34 +299,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
           }
           val = {e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16)};
         }
-        // keys past the largest limit may hold anything (NaN bits included);
-        // they are zeroed when the registers go to LDS, so no wait here
-        r.v_valid[j] = max_lim - tok;
-        r.v[j] = val;
-      }
-    }
-  };
-  auto store_step = [&](const StepRegs<HD>& r, int buf) {
-    uint16_t* kl = k_lds(buf);
-    uint16_t* vl = v_lds(buf);
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      const int i = tid + j * kPfThreads;
-      if (i < HD * 4) {
-        int c, kj, d, kg;
-        k_item(i, c, kj);
-        v_item(i, d, kg);
-        *reinterpret_cast<u32x4*>(kl + (c * kKeys + kj) * 8) = r.k[j];
-        u32x4 v = r.v[j];
-        const int valid = r.v_valid[j];
+        // keys past the largest limit may hold anything (NaN bits included)
+        const int valid = max_lim - tok;
         if (valid < 8) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t keep = (2 * e < valid ? 0x0000FFFFu : 0u) | (2 * e + 1 < valid ? 0xFFFF0000u : 0u);
-            v[e] &= keep;
+            val[e] &= keep;
           }
         }
-        *reinterpret_cast<u32x4*>(vl + d * kVRow + kg) = v;
+        *reinterpret_cast<u32x4*>(v_lds(buf) + i * 8) = val;
       }
     }
   };
@@ -282,29 +321,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[n][r] = 0.f;
 
-  // Pipeline: while step st is computed from LDS, the K/V loads of step st+1
-  // are in flight in registers and the page ids of step st+2 in two more;
-  // after the compute the registers go to the other LDS buffer, the loads of
-  // step st+2 and the page ids of step st+3 are issued, and one barrier ends
-  // the step.
-  const int nsteps = (max_lim + kKeys - 1) / kKeys;
-  StepRegs<HD> regs;
-  uint32_t pga = 0xFFFFFFFFu, pgb = 0xFFFFFFFFu;
-  if (nsteps > 0) {
-    load_pages(0, pga, pgb);
-    load_step(0, regs, pga, pgb);
-    store_step(regs, 0);
-    if (nsteps > 1) {
-      load_pages(kKeys, pga, pgb);
-      load_step(kKeys, regs, pga, pgb);
-      if (nsteps > 2) load_pages(2 * kKeys, pga, pgb);
-    }
-  }
-  __syncthreads();
-  for (int st = 0; st < nsteps; ++st) {
-    const int buf = st & 1;
-    const int k0 = st * kKeys;
+  // Key order inside a 32-key step.  The QK product's A operand takes key
+  // kperm(m) as its row m (bits 2 and 3 of m swapped); then the 8 scores a
+  // lane feeds into each PV k-step are 8 consecutive keys, and the V^T operand
+  // is one 16-byte LDS read per lane.
+  auto kperm = [](int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); };
+  const int kcol = kperm(col);
 
+  auto compute_step = [&](int st) {
+    const int buf = st % kNBuf;
+    const int k0 = st * kKeys;
     // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d]
     f32x16 sacc;
 #pragma unroll
@@ -312,23 +338,23 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       const int c = 2 * kk + half;  // stripe of dims 16kk + 8 half .. +7
-      const u32x4 ka = *reinterpret_cast<const u32x4*>(k_lds(buf) + (c * kKeys + col) * 8);
+      const u32x4 ka = *reinterpret_cast<const u32x4*>(k_lds(buf) + IM::k_slot(kcol, c) * 8);
       sacc = Dt<DT>::mma32x32x16(ka, qv[kk], sacc);
     }
-    // lane holds keys k0 + 8 (r/4) + 4 half + r%4 of M-row col.  Scores stay
-    // raw (the scale is positive, so maxima commute with it); the exponent is
-    // one fma: s * scale_log2 - m * scale_log2.
+    // register r holds key k0 + 16 (r/8) + 8 half + 4 ((r/4)%2) + r%4 of
+    // M-row col.  Scores stay raw (the scale is positive, so maxima commute
+    // with it); the exponent is one fma: s * scale_log2 - m * scale_log2.
     float bm = -INFINITY;
     if (k0 + kKeys > min_lim) {  // some key of this step is masked for some row
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const int key = k0 + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
         if (key >= my_lim) sacc[r] = -INFINITY;
       }
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[r]);
-    bm = fmaxf(bm, shfl_xor(bm, 32));
+    bm = max_xor32(bm);
     if (__ballot(bm > m_run + kLazyRescale * p.scale_inv_log2)) {
       const bool grow = bm > m_run + kLazyRescale * p.scale_inv_log2;
       const float m_new = fmaxf(m_run, bm);
@@ -347,8 +373,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       pe[r] = __builtin_amdgcn_exp2f(fmaf(sacc[r], p.scale_log2, mb));
       l_run += pe[r];
     }
-    // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk covers the
-    // keys held in registers 8kk .. 8kk+7: {16kk + 4 half + e, 16kk + 8 + 4 half + e}.
+    // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
+    // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const u32x4 pb = {Dt<DT>::pack2(pe[8 * kk + 0], pe[8 * kk + 1]), Dt<DT>::pack2(pe[8 * kk + 2], pe[8 * kk + 3]),
@@ -356,25 +382,51 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
       for (int n = 0; n < DT32; ++n) {
         const int d = 32 * n + col;
-        const uint16_t* vrow = v_lds(buf) + d * kVRow + 16 * kk + 4 * half;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-        const u32x4 va = {lo.x, lo.y, hi.x, hi.y};
+        const u32x4 va = *reinterpret_cast<const u32x4*>(v_lds(buf) + IM::v_slot(d, 16 * kk + 8 * half) * 8);
         o[n] = Dt<DT>::mma32x32x16(va, pb, o[n]);
       }
     }
-    if (st + 1 < nsteps) {
-      store_step(regs, buf ^ 1);  // buffer buf^1 was last read in step st-1, before the last barrier
-      if (st + 2 < nsteps) {
-        load_step(k0 + 2 * kKeys, regs, pga, pgb);
-        if (st + 3 < nsteps) load_pages(k0 + 3 * kKeys, pga, pgb);
+  };
+
+  // Pipeline: steps st+1 and st+2 are in flight (direct-to-LDS) while step st
+  // is computed; four buffers, because a straggling wavefront may still read
+  // step st-1 when the copies of step st+2 start.  The wait before each
+  // step's barrier lets the 2*NL (one step) or 4*NL (two steps) youngest
+  // copies stay in flight.
+  if (nsteps > 0) {
+    stage_pids(0);
+    if (n_pid > kPidChunk) stage_pids(1);
+  }
+  __syncthreads();
+  if (nsteps > 0) issue(0);
+  if (nsteps > 1) issue(1);
+  for (int st = 0; st < nsteps; ++st) {
+    const int j = st + 2;
+    if (j < nsteps) {
+      // entering page-id chunk q (q >= 1): stage chunk q + 1 over chunk q - 1,
+      // whose last reader was at least one barrier ago
+      const int e0 = j * kKeys / TPP;
+      if (e0 % kPidChunk == 0 && e0 > 0 && e0 + kPidChunk < n_pid) {
+        stage_pids(e0 / kPidChunk + 1);
+        __syncthreads();
       }
+      issue(j);
     }
-    __syncthreads();
+    asm volatile("" ::: "memory");
+    if (st + 2 < nsteps)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NL));
+    else if (st + 1 < nsteps)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __builtin_amdgcn_s_waitcnt(kLgkmZero);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    compute_step(st);
   }
 
   // ---- normalise and write: lane holds O[M-row col][32n + 8(r/4) + 4 half + r%4]
-  float l = l_run + shfl_xor(l_run, 32);
+  float l = sum_xor32(l_run);
   if (row_ok) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int64_t orow = static_cast<int64_t>(row0 + my_t) * p.num_q_heads + kvh * p.group + h0 + my_h;
@@ -410,8 +462,10 @@ __device__ __forceinline__ bool single_row(const uint32_t* q2seq, int64_t r, int
 //    row is computed as a tile.
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * HD * kKeys];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * HD * (kKeys + kVPad)];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kNBuf * StepGeo<HD>::kItems * 8];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kNBuf * StepGeo<HD>::kItems * 8];
+  __shared__ __attribute__((aligned(16))) uint16_t junk_lds[kWave * 8];  // target of the padding copies
+  __shared__ uint32_t pid_lds[2 * kPidChunk];
   __shared__ int lim_lds[kMRows];
   __shared__ int run_start[kMRows];
   const int G = p.num_kv_heads * p.head_chunks;
@@ -425,7 +479,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillP
     const int s = unit / tps;
     const int j = tps - 1 - (unit - s * tps);
     const int row0 = s * p.prompt_len + j * qt;
-    prefill_tile<DT, HD, TPP, true>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, lim_lds);
+    prefill_tile<DT, HD, TPP, true>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, junk_lds,
+                                    pid_lds, lim_lds);
     return;
   }
   const int w0 = unit * qt;
@@ -439,7 +494,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillP
     while (end < w1 && !run_start[end - w0]) ++end;
     end = __builtin_amdgcn_readfirstlane(end);
     if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
-      prefill_tile<DT, HD, TPP, false>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, lim_lds);
+      prefill_tile<DT, HD, TPP, false>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
+                                       lim_lds);
     cur = end;
   }
 }
