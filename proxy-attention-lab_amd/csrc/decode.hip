@@ -41,7 +41,9 @@
 //  * A segment that lies wholly inside one virtual worker writes the
 //    normalised output directly.  Split segments leave fp32 partials
 //    (max, exp-sum, unnormalised O) in one of two slots per virtual worker,
-//    combined by decode_merge_kernel, which also re-arms the claim counter.
+//    combined by decode_merge_kernel.  The worker holding the first piece of
+//    a split segment writes it into its own slot of a merge list, so the
+//    merge grid does not grow with the batch.
 #include "pal_device.h"
 
 #ifndef PAL_DECODE_PREFETCH
@@ -56,6 +58,7 @@ constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgr
 constexpr int kGroupThreads = kWorkersPerGroup * kWave;
 constexpr int kPlanThreads = 1024;
 constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each workgroup
+constexpr int64_t kMergeGroups = 2048;  // merge grid (at most): workgroups stride over the list
 #ifndef PAL_DECODE_STATIC_SHARE
 #define PAL_DECODE_STATIC_SHARE 4  // static quarters of the block list (4 = all static)
 #endif
@@ -143,6 +146,15 @@ __device__ __forceinline__ int64_t vworker_of(const Sched& sc, int64_t b) {
   return sc.nws + (b - sc.ts) / sc.chunk;
 }
 
+// Zeros for every head of an empty item (no visible key).  Run by the
+// planner's thread that finds the item; such items are rare.
+template <int HD>
+__device__ __forceinline__ void zero_item_output(const DecodeParams& p, int64_t row) {
+  u32x2* o = reinterpret_cast<u32x2*>(p.out + row * p.num_q_heads * HD);  // out is 8-byte aligned
+  const int64_t n = static_cast<int64_t>(p.num_q_heads) * HD / 4;
+  for (int64_t i = 0; i < n; ++i) o[i] = u32x2{0u, 0u};
+}
+
 // Sequence holding global block b: the largest s with cum[s] <= b.
 __device__ __forceinline__ int64_t locate_seq(const int64_t* cum, int64_t num_seqs, int64_t b) {
   int64_t lo = 0, hi = num_seqs - 1;
@@ -154,8 +166,12 @@ __device__ __forceinline__ int64_t locate_seq(const int64_t* cum, int64_t num_se
 }
 
 // Scan for batches larger than kInlinePlanSeqs: cum[s] = first global block of
-// sequence s (all of its segments), cum[S] = hdr[0] = T.
-template <int TPP>
+// sequence s (all of its segments), cum[S] = hdr[0] = T.  Each thread takes
+// kPlanPer consecutive items per pass, so their length loads go out together;
+// it also writes the zeros of an empty item.
+constexpr int kPlanPer = 8;
+
+template <int HD, int TPP>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeParams p) {
   __shared__ int64_t wave_sums[kPlanThreads / kWave];
   __shared__ int64_t carry_sh;
@@ -163,11 +179,28 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   const int tid = threadIdx.x;
   int64_t carry = 0;
   const int64_t n = p.num_seqs;
-  for (int64_t base = 0; base < n; base += kPlanThreads) {
-    const int64_t s = base + tid;
-    const int64_t v = s < n ? seq_blocks(p, s, TPP) * segs : 0;
-    const int64_t inc = block_inclusive_scan<kPlanThreads>(v, wave_sums);
-    if (s < n) p.cum[s] = carry + inc - v;
+  for (int64_t base = 0; base < n; base += static_cast<int64_t>(kPlanThreads) * kPlanPer) {
+    int64_t vals[kPlanPer];
+    int64_t tsum = 0;
+#pragma unroll
+    for (int k = 0; k < kPlanPer; ++k) {
+      const int64_t s = base + static_cast<int64_t>(tid) * kPlanPer + k;
+      vals[k] = 0;
+      if (s < n) {
+        const Item it = item_at(p, s, TPP);
+        vals[k] = ((it.len + 15) >> 4) * segs;
+        if (it.len == 0 && !it.skip) zero_item_output<HD>(p, it.row);
+      }
+      tsum += vals[k];
+    }
+    const int64_t inc = block_inclusive_scan<kPlanThreads>(tsum, wave_sums);
+    int64_t c = carry + inc - tsum;
+#pragma unroll
+    for (int k = 0; k < kPlanPer; ++k) {
+      const int64_t s = base + static_cast<int64_t>(tid) * kPlanPer + k;
+      if (s < n) p.cum[s] = c;
+      c += vals[k];
+    }
     if (tid == kPlanThreads - 1) carry_sh = inc;
     __syncthreads();
     carry += carry_sh;
@@ -200,7 +233,14 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 
   const int64_t b0 = vstart(sc, v);
   int64_t remaining = vstart(sc, v + 1) - b0;
-  if (remaining <= 0) return;
+  // merge-list slot of this virtual worker: written exactly once per call
+  // (the split segment whose first piece ends this range, or 0), so the slot
+  // never depends on what an earlier call left in the workspace
+  int64_t list_g0 = -1, list_nb = 0, list_row = 0, list_seg = 0;  // g0 < 0: nothing to merge
+  if (remaining <= 0) {
+    if (lane_id() == 0 && v < p.list_cap) p.split_list[4 * v] = -1;
+    return;
+  }
   int64_t s = locate_seq(cum, n_items, b0);
   int64_t r = b0 - cum[s];
 
@@ -211,6 +251,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;  // elements per (page, kv head)
   const int64_t page_stride = head_block * p.num_kv_heads;
   bool first = true;
+  int64_t gpos = b0;  // global block at which the current piece starts
 
   while (remaining > 0) {
     const Item it = item_at(p, s, TPP);
@@ -386,13 +427,30 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       }
     }
 
+    // the first piece of a split segment can only end the range (a range
+    // ends inside one segment): that segment goes on the merge list
+    if (!complete && blk == 0) {
+      list_g0 = gpos;  // the piece starts the segment
+      list_nb = nb;
+      list_row = it.row;
+      list_seg = seg;
+    }
+
     remaining -= count;
+    gpos += count;
     r += count;
     if (r >= nb * segs) {
       ++s;
       r = 0;
     }
     first = false;
+  }
+  if (lane_id() == 0 && v < p.list_cap) {
+    int64_t* slot = p.split_list + 4 * v;
+    slot[0] = list_g0;
+    slot[1] = list_nb;
+    slot[2] = list_row;
+    slot[3] = list_seg;
   }
 }
 
@@ -416,7 +474,13 @@ void decode_stream_kernel(const DecodeParams p) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int64_t s = static_cast<int64_t>(tid) * kPer + k;
-      vals[k] = s < n_items ? seq_blocks(p, s, TPP) * segs : 0;
+      vals[k] = 0;
+      if (s < n_items) {
+        const Item it = item_at(p, s, TPP);
+        vals[k] = ((it.len + 15) >> 4) * segs;
+        // empty items get zeros, written once, by workgroup 0
+        if (it.len == 0 && !it.skip && blockIdx.x == 0) zero_item_output<HD>(p, it.row);
+      }
       tsum += vals[k];
     }
     const int64_t incl = block_inclusive_scan<kGroupThreads>(tsum, wave_sums);
@@ -451,90 +515,86 @@ void decode_stream_kernel(const DecodeParams p) {
   }
 }
 
-// One wavefront per (sequence, query head): combines the partials of a
-// segment that several virtual workers shared, M = max_c m_c,
-// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  Lane j fetches the
-// (m, l) of the j-th contributor so those loads go out together; the O loads
-// of consecutive contributors are unrolled to keep several in flight.
-// Empty sequences get zeros; segments finished by one worker are already out.
-// The first thread re-arms the claim counter for the next call.
+// Walks the merge list, slot v for virtual worker v (first block < 0:
+// nothing to merge; every slot of the live range was written by this call's
+// workers, with the segment's first block, block count, output row and
+// segment index, so the merge needs no other lookup);
+// a workgroup per slot at a time, the grid striding over the live workers.
+// A split segment (sequence, kv head, head chunk) is merged head by head, a
+// wavefront per head: M = max_c m_c, out = sum_c 2^(m_c - M) O_c /
+// sum_c 2^(m_c - M) l_c over the virtual workers c that shared it.  Lane j
+// fetches the (m, l) of the j-th contributor so those loads go out together;
+// the O loads of consecutive contributors are unrolled to keep several in
+// flight.  Workgroup 0 re-arms the claim counter.
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
-  const int64_t wrow = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (wrow >= p.num_seqs * p.num_q_heads) return;
-  const int64_t s = wrow / p.num_q_heads;
-  const int qh = static_cast<int>(wrow - s * p.num_q_heads);
-  const Item it = item_at(p, s, TPP);
-  if (it.skip) return;
-  const int64_t row = it.row * p.num_q_heads + qh;  // output row
   const int lane = lane_id();
+  const int wv = wave_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
-  const int64_t nb = (it.len + 15) >> 4;
   const int64_t total = p.hdr[0];
-  const int64_t cum_s = p.cum[s];
-  if (nb == 0) {
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      const int d = lane + e * kWave;
-      if (d < HD) p.out[row * HD + d] = 0;
-    }
-    return;
-  }
+  if (total == 0) return;
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
-  const int kvh = qh / p.group;
-  const int hl = qh - kvh * p.group;
-  const int seg = kvh * p.head_chunks + hl / 16;
-  const int h = hl % 16;
-  const int64_t g0 = cum_s + seg * nb;
-  const int64_t v0 = vworker_of(sc, g0);
-  const int64_t v1 = vworker_of(sc, g0 + nb - 1);
-  if (v0 == v1) return;
-  const int64_t n = v1 - v0 + 1;
+  const int64_t n_slots = sc.nws + sc.nc < p.list_cap ? sc.nws + sc.nc : p.list_cap;
+  for (int64_t e = blockIdx.x; e < n_slots; e += gridDim.x) {
+    const int64_t* slot = p.split_list + 4 * e;
+    const int64_t g0 = slot[0];
+    if (g0 < 0) continue;
+    const int64_t nb = slot[1];
+    const int64_t out_row = slot[2];
+    const int seg = static_cast<int>(slot[3]);
+    const int kvh = seg / p.head_chunks;
+    const int h0 = (seg % p.head_chunks) * 16;
+    const int hg = min(16, p.group - h0);
+    const int64_t v0 = vworker_of(sc, g0);
+    const int64_t v1 = vworker_of(sc, g0 + nb - 1);
+    const int64_t nc = v1 - v0 + 1;
+    for (int h = wv; h < hg; h += kWorkersPerGroup) {
+      const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
+      auto slot_of = [&](int64_t u) { return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h; };
 
-  auto slot_of = [&](int64_t u) { return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h; };
+      float big_m = -INFINITY;
+      for (int64_t base = 0; base < nc; base += kWave) {
+        const int64_t j = base + lane;
+        const float m = j < nc ? p.part_ml[slot_of(v0 + j) * 2] : -INFINITY;
+        big_m = fmaxf(big_m, m);
+      }
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) big_m = fmaxf(big_m, shfl_xor(big_m, off));
+      const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
 
-  float big_m = -INFINITY;
-  for (int64_t base = 0; base < n; base += kWave) {
-    const int64_t j = base + lane;
-    const float m = j < n ? p.part_ml[slot_of(v0 + j) * 2] : -INFINITY;
-    big_m = fmaxf(big_m, m);
-  }
+      float lsum = 0.f;
+      float acc[kPer];
 #pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) big_m = fmaxf(big_m, shfl_xor(big_m, off));
-  const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
-
-  float lsum = 0.f;
-  float acc[kPer];
+      for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
+      for (int64_t base = 0; base < nc; base += kWave) {
+        const int64_t j = base + lane;
+        float wgt = 0.f;
+        if (j < nc) {
+          const int64_t sl = slot_of(v0 + j);
+          wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
+          lsum += wgt * p.part_ml[sl * 2 + 1];
+        }
+        const int cnt = static_cast<int>((nc - base) < kWave ? (nc - base) : kWave);
+        for (int jj = 0; jj < cnt; ++jj) {
+          const float wj = __shfl(wgt, jj, kWave);
+          const float* po = p.part_o + slot_of(v0 + base + jj) * HD;
 #pragma unroll
-  for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
-  for (int64_t base = 0; base < n; base += kWave) {
-    const int64_t j = base + lane;
-    float wgt = 0.f;
-    if (j < n) {
-      const int64_t sl = slot_of(v0 + j);
-      wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
-      lsum += wgt * p.part_ml[sl * 2 + 1];
-    }
-    const int cnt = static_cast<int>((n - base) < kWave ? (n - base) : kWave);
-#pragma unroll 8
-    for (int jj = 0; jj < cnt; ++jj) {
-      const float wj = __shfl(wgt, jj, kWave);
-      const float* po = p.part_o + slot_of(v0 + base + jj) * HD;
+          for (int q = 0; q < kPer; ++q) {
+            const int d = lane + q * kWave;
+            if (d < HD) acc[q] += wj * po[d];
+          }
+        }
+      }
 #pragma unroll
-      for (int e = 0; e < kPer; ++e) {
-        const int d = lane + e * kWave;
-        if (d < HD) acc[e] += wj * po[d];
+      for (int off = 1; off < kWave; off <<= 1) lsum += shfl_xor(lsum, off);
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int d = lane + q * kWave;
+        if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
       }
     }
-  }
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) lsum += shfl_xor(lsum, off);
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int d = lane + e * kWave;
-    if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[e] * inv);
   }
 }
 
@@ -542,7 +602,7 @@ template <int DT, int HD, int TPP>
 hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   hipError_t err;
   if (p.num_seqs > kInlinePlanSeqs) {
-    hipLaunchKernelGGL((decode_plan_kernel<TPP>), dim3(1), dim3(kPlanThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_plan_kernel<HD, TPP>), dim3(1), dim3(kPlanThreads), 0, stream, p);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -551,9 +611,8 @@ hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
                      0, stream, p);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
-  const int64_t rows = p.num_seqs * p.num_q_heads;
-  hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>),
-                     dim3(static_cast<unsigned>((rows + kWorkersPerGroup - 1) / kWorkersPerGroup)),
+  const int64_t merge_groups = p.list_cap < kMergeGroups ? p.list_cap : kMergeGroups;
+  hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(merge_groups)),
                      dim3(kGroupThreads), 0, stream, p);
   return hipGetLastError();
 }

@@ -59,9 +59,11 @@ bool decode_partition_ok(int partition_size) {
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
 // Decode workspace layout (all offsets 256-aligned).  The claim counter at
-// byte 64 must be zero when a call starts; every call leaves it zero.
+// byte 64 must be zero when a call starts; every call leaves it zero.  Every
+// other byte is scratch that each call writes before it reads.
 struct DecodeLayout {
-  size_t hdr, claim, cum, part_ml, part_o, total;
+  size_t hdr, claim, cum, list, part_ml, part_o, total;
+  int64_t list_cap;
 };
 
 DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t virtual_workers) {
@@ -72,6 +74,10 @@ DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t v
   off += 256;
   l.cum = off;
   off += align256(static_cast<size_t>(num_seqs + 1) * sizeof(int64_t));
+  // merge list: one slot per virtual worker
+  l.list_cap = virtual_workers;
+  l.list = off;
+  off += align256(static_cast<size_t>(l.list_cap) * 4 * sizeof(int64_t));
   l.part_ml = off;
   off += align256(static_cast<size_t>(virtual_workers) * 2 * hg_max * 2 * sizeof(float));
   l.part_o = off;
@@ -125,6 +131,8 @@ pal::DecodeParams decode_params(const void* queries, const void* k_pool, const v
   p.num_pt_rows = num_items;
   p.hdr = reinterpret_cast<int64_t*>(ws + lay.hdr);
   p.claim = reinterpret_cast<uint32_t*>(ws + lay.claim);
+  p.split_list = reinterpret_cast<int64_t*>(ws + lay.list);
+  p.list_cap = lay.list_cap;
   p.cum = reinterpret_cast<int64_t*>(ws + lay.cum);
   p.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
   p.part_o = reinterpret_cast<float*>(ws + lay.part_o);

@@ -51,6 +51,10 @@ struct DecodeParams {
   // workspace
   int64_t* hdr;                // hdr[0] = total blocks T
   uint32_t* claim;             // dynamic-chunk counter: 0 on entry, re-armed to 0 by the merge kernel
+  int64_t* split_list;         // [list_cap][4] per virtual worker: {first block (< 0: none), blocks,
+                               // output row, segment} of the split segment its range ends in
+                               // (every live slot is written by each call before the merge reads it)
+  int64_t list_cap;
   int64_t* cum;                // [S + 1] first global block of each sequence
   float* part_ml;              // [virtual workers][2][hg_max][2] (max * log2e * scale, exp-sum)
   float* part_o;               // [virtual workers][2][hg_max][HD]  unnormalised O
