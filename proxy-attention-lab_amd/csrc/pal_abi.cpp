@@ -2,13 +2,16 @@
 //
 // Replaces the reference's binding + primitive host layers
 // (src/pal_core/bindings.cpp, src/pal_core/src/ops.cpp,
-// src/pal_core/src/*_primitive.cpp).  The library is stateless apart from a
-// thread-local error message; it never allocates device memory.
+// src/pal_core/src/*_primitive.cpp).  The library keeps a thread-local error
+// message and, per device, the fused op's side stream and its two events; it
+// never allocates device memory.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "../../include/pal_hip.h"
@@ -110,6 +113,32 @@ int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seq
   *resident = res;
   *virtual_workers = vw;
   return PAL_OK;
+}
+
+// Side stream of the fused op, one per device: the prefill tiles (MFMA-bound)
+// run on it while the decode rows (HBM-bound) run on the caller's stream, so
+// the two halves of a mixed batch overlap.  Fork and join are event waits,
+// which stream capture records like any other dependency.  Default priority.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+};
+std::mutex g_side_mu;
+std::map<int, SideStream> g_side;
+
+hipError_t side_stream(int device, SideStream** out) {
+  SideStream& ss = g_side[device];
+  if (!ss.stream) {
+    hipError_t err = hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking);
+    if (err != hipSuccess) return err;
+    err = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming);
+    if (err != hipSuccess) return err;
+    err = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming);
+    if (err != hipSuccess) return err;
+  }
+  *out = &ss;
+  return hipSuccess;
 }
 
 // Common decode parameter set-up (plain decode: item i = row i = sequence i).
@@ -449,9 +478,6 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   pp.hg_max = hg_max;
   pp.scale_log2 = scale_log2_for(head_dim);
   pp.scale_inv_log2 = 1.f / pp.scale_log2;
-  hipError_t err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, hs);
-  if (err != hipSuccess) return hip_status(err, op);
-
   // 2. rows alone in their run: split-K decode
   pal::DecodeParams dp = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
                                        static_cast<char*>(workspace), lay, num_query_rows, num_pages,
@@ -459,7 +485,28 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   dp.q2seq = query_to_seq_map;
   dp.q_offset = query_token_offset;
   dp.num_pt_rows = num_seqs;
-  return hip_status(pal::launch_decode(dp, dtype, head_dim, tokens_per_page, hs), op);
+
+  // The decode grid (one persistent workgroup per CU) is launched first on
+  // the caller's stream, then the prefill tiles on the side stream fill the
+  // remaining slots; the caller's stream waits for both.
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, op);
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream* ss = nullptr;
+  err = side_stream(dev, &ss);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = hipEventRecord(ss->fork, hs);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = hipStreamWaitEvent(ss->stream, ss->fork, 0);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = pal::launch_decode(dp, dtype, head_dim, tokens_per_page, hs);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, ss->stream);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = hipEventRecord(ss->join, ss->stream);
+  if (err != hipSuccess) return hip_status(err, op);
+  return hip_status(hipStreamWaitEvent(hs, ss->join, 0), op);
 }
 
 }  // extern "C"
