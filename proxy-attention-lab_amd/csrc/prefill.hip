@@ -62,21 +62,39 @@ struct StepGeo {
 // so one direct-to-LDS load per wavefront fills 1 KiB of consecutive slots
 // (lane l -> slot base + l).  With TPP 16 the items are page-major (2*HD per
 // page), which also makes each load instruction read a single page.
-//   K item i: stripe c, key t within the page half ph:     page offset (c*TPP + t) * 8
-//   V item i: row d, 8-key group g' = g ^ swz(d) of the row: page offset d*TPP + 8 g'
-// The V groups are swizzled by row so that the PV operand reads (8 rows x 16
-// bytes per 8-lane group) hit 32 distinct banks.
+//   K item i: stripe c, slot t of the step holds key kperm(t):  page offset (c*TPP + kperm(t) % TPP) * 8
+//   V item i: row d, 8-key group g' = g ^ swz(d) of the row:     page offset d*TPP + 8 g'
+// K keys are stored in the QK operand's row order (kperm, an involution
+// swapping bits 2 and 3 of the key index), so the operand reads are
+// contiguous; the V groups are swizzled by row so that the PV operand reads
+// (one 16-byte chunk per lane and row) spread over all banks.
+__device__ __forceinline__ int kperm(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
 template <int HD, int TPP>
 struct ItemMap {
   static __device__ __forceinline__ int k_page_half(int i) { return TPP == 16 ? i / (2 * HD) : 0; }
-  static __device__ __forceinline__ int k_offset(int i) {  // element offset inside the (page, kv head) block
+  // K item i: stripe c and the key (within the step) it carries
+  static __device__ __forceinline__ void k_item(int i, int& c, int& key) {
     if (TPP == 16) {
       const int rem = i % (2 * HD);
-      return ((rem / 16) * TPP + rem % 16) * 8;
+      c = rem / 16;
+      key = (i / (2 * HD)) * 16 + kperm(rem % 16);
+    } else {
+      c = i / 32;
+      key = kperm(i % 32);
     }
-    return ((i / 32) * TPP + i % 32) * 8;
   }
-  static __device__ __forceinline__ int v_swz(int d) { return TPP == 16 ? (d >> 2) & 1 : (d >> 1) & 3; }
+  static __device__ __forceinline__ int k_offset(int i) {  // element offset inside the (page, kv head) block
+    int c, key;
+    k_item(i, c, key);
+    return (c * TPP + key % TPP) * 8;
+  }
+  // Conflict-free for 8-lane groups over 32 banks and 16-lane groups over 64
+  // banks: within any 8 (and any 16) consecutive rows the 16-byte chunk each
+  // lane reads lands on a distinct bank group.
+  static __device__ __forceinline__ int v_swz(int d) {
+    return TPP == 16 ? ((d >> 2) ^ (d >> 3)) & 1 : ((d >> 1) ^ (d >> 3)) & 3;
+  }
   // V item i: row d and the group g stored in its slot (key offset in the step)
   static __device__ __forceinline__ void v_item(int i, int& d, int& key) {
     if (TPP == 16) {
@@ -88,9 +106,9 @@ struct ItemMap {
       key = 8 * ((i % 4) ^ v_swz(d));
     }
   }
-  // LDS slot of K (key kj of the step, stripe c)
-  static __device__ __forceinline__ int k_slot(int kj, int c) {
-    return TPP == 16 ? (kj / 16) * (2 * HD) + c * 16 + kj % 16 : c * 32 + kj;
+  // LDS slot of K operand row m (key kperm(m) of the step), stripe c
+  static __device__ __forceinline__ int k_slot(int m, int c) {
+    return TPP == 16 ? (m / 16) * (2 * HD) + c * 16 + m % 16 : c * 32 + m;
   }
   // LDS slot holding V row d, keys kg .. kg+7 of the step (kg multiple of 8)
   static __device__ __forceinline__ int v_slot(int d, int kg) {
@@ -256,14 +274,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       // K: stripe c, key kj of the step
       {
         int kj, c;
-        if (TPP == 16) {
-          const int rem = i % (2 * HD);
-          c = rem / 16;
-          kj = (i / (2 * HD)) * 16 + rem % 16;
-        } else {
-          c = i / 32;
-          kj = i % 32;
-        }
+        IM::k_item(i, c, kj);
         const int tok = k0 + kj;
         u32x4 val = {0u, 0u, 0u, 0u};
         if (!prompt_mode || tok < hist) {
@@ -324,26 +335,24 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // Key order inside a 32-key step.  The QK product's A operand takes key
   // kperm(m) as its row m (bits 2 and 3 of m swapped); then the 8 scores a
   // lane feeds into each PV k-step are 8 consecutive keys, and the V^T operand
-  // is one 16-byte LDS read per lane.
-  auto kperm = [](int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); };
-  const int kcol = kperm(col);
+  // is one 16-byte LDS read per lane.  LDS already holds K in this row order.
 
-  auto compute_step = [&](int st) {
+  // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d] for step st (raw scores).
+  auto read_k = [&](int st, u32x4 (&ka)[KS]) {
     const int buf = st % kNBuf;
-    const int k0 = st * kKeys;
-    // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d]
-    f32x16 sacc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       const int c = 2 * kk + half;  // stripe of dims 16kk + 8 half .. +7
-      const u32x4 ka = *reinterpret_cast<const u32x4*>(k_lds(buf) + IM::k_slot(kcol, c) * 8);
-      sacc = Dt<DT>::mma32x32x16(ka, qv[kk], sacc);
+      ka[kk] = *reinterpret_cast<const u32x4*>(k_lds(buf) + IM::k_slot(col, c) * 8);
     }
-    // register r holds key k0 + 16 (r/8) + 8 half + 4 ((r/4)%2) + r%4 of
-    // M-row col.  Scores stay raw (the scale is positive, so maxima commute
-    // with it); the exponent is one fma: s * scale_log2 - m * scale_log2.
+  };
+  // register r holds key k0 + 16 (r/8) + 8 half + 4 ((r/4)%2) + r%4 of
+  // M-row col.  Scores stay raw (the scale is positive, so maxima commute
+  // with it); the exponent is one fma: s * scale_log2 - m * scale_log2.
+  // Masks the step's scores, moves the running max if needed (lazily) and
+  // returns the exponent offset.
+  auto mask_and_max = [&](f32x16& sacc, int st) {
+    const int k0 = st * kKeys;
     float bm = -INFINITY;
     if (k0 + kKeys > min_lim) {  // some key of this step is masked for some row
 #pragma unroll
@@ -366,40 +375,42 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
       for (int n = 0; n < DT32; ++n) o[n] *= a;
     }
-    const float mb = (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
-    float pe[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      pe[r] = __builtin_amdgcn_exp2f(fmaf(sacc[r], p.scale_log2, mb));
-      l_run += pe[r];
-    }
-    // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
-    // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const u32x4 pb = {Dt<DT>::pack2(pe[8 * kk + 0], pe[8 * kk + 1]), Dt<DT>::pack2(pe[8 * kk + 2], pe[8 * kk + 3]),
-                        Dt<DT>::pack2(pe[8 * kk + 4], pe[8 * kk + 5]), Dt<DT>::pack2(pe[8 * kk + 6], pe[8 * kk + 7])};
-#pragma unroll
-      for (int n = 0; n < DT32; ++n) {
-        const int d = 32 * n + col;
-        const u32x4 va = *reinterpret_cast<const u32x4*>(v_lds(buf) + IM::v_slot(d, 16 * kk + 8 * half) * 8);
-        o[n] = Dt<DT>::mma32x32x16(va, pb, o[n]);
-      }
-    }
+    return (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
   };
 
-  // Pipeline: steps st+1 and st+2 are in flight (direct-to-LDS) while step st
-  // is computed; four buffers, because a straggling wavefront may still read
-  // step st-1 when the copies of step st+2 start.  The wait before each
-  // step's barrier lets the 2*NL (one step) or 4*NL (two steps) youngest
-  // copies stay in flight.
+  // Pipeline.  Memory: steps st+1 and st+2 are in flight (direct-to-LDS)
+  // while step st is computed; four buffers, because a straggling wavefront
+  // may still read steps st and st+1 when the copies of step st+2 start.
+  // Compute: inside a wavefront, the QK MFMAs of step st+1 are interleaved
+  // with the exponentials of step st (independent work for the matrix and
+  // vector units), then the PV MFMAs of step st follow.
   if (nsteps > 0) {
     stage_pids(0);
     if (n_pid > kPidChunk) stage_pids(1);
   }
   __syncthreads();
-  if (nsteps > 0) issue(0);
-  if (nsteps > 1) issue(1);
+  auto wait_barrier = [&](int pending_steps) {  // all but the pending_steps youngest steps' copies landed
+    asm volatile("" ::: "memory");
+    if (pending_steps >= 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __builtin_amdgcn_s_waitcnt(kLgkmZero);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  f32x16 s_cur;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s_cur[r] = 0.f;
+  if (nsteps > 0) {
+    issue(0);
+    if (nsteps > 1) issue(1);
+    wait_barrier(nsteps > 1 ? 1 : 0);
+    u32x4 ka[KS];
+    read_k(0, ka);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) s_cur = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_cur);
+  }
   for (int st = 0; st < nsteps; ++st) {
     const int j = st + 2;
     if (j < nsteps) {
@@ -412,17 +423,46 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       }
       issue(j);
     }
-    asm volatile("" ::: "memory");
-    if (st + 2 < nsteps)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NL));
-    else if (st + 1 < nsteps)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    __builtin_amdgcn_s_waitcnt(kLgkmZero);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    compute_step(st);
+    wait_barrier(j < nsteps ? 1 : 0);  // step st+1 has landed
+
+    const float mb = mask_and_max(s_cur, st);
+    // (on the last step the "next" QK reads a stale, in-bounds buffer and its
+    // result is dropped: one extra QK per tile keeps the region branch-free)
+    u32x4 ka[KS];
+    read_k(st + 1, ka);
+    u32x4 va[2][DT32];
+    {
+      const int buf = st % kNBuf;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int n = 0; n < DT32; ++n)
+          va[kk][n] = *reinterpret_cast<const u32x4*>(v_lds(buf) + IM::v_slot(32 * n + col, 16 * kk + 8 * half) * 8);
+    }
+    // QK of step st+1 (matrix unit) alongside the exponentials of step st
+    f32x16 s_next;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) s_next = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_next);
+    float pe[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      pe[r] = __builtin_amdgcn_exp2f(fmaf(s_cur[r], p.scale_log2, mb));
+      l_run += pe[r];
+    }
+    u32x4 pb[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      pb[kk] = u32x4{Dt<DT>::pack2(pe[8 * kk + 0], pe[8 * kk + 1]), Dt<DT>::pack2(pe[8 * kk + 2], pe[8 * kk + 3]),
+                     Dt<DT>::pack2(pe[8 * kk + 4], pe[8 * kk + 5]), Dt<DT>::pack2(pe[8 * kk + 6], pe[8 * kk + 7])};
+    // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
+    // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int n = 0; n < DT32; ++n) o[n] = Dt<DT>::mma32x32x16(va[kk][n], pb[kk], o[n]);
+    s_cur = s_next;
   }
 
   // ---- normalise and write: lane holds O[M-row col][32n + 8(r/4) + 4 half + r%4]
