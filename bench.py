@@ -75,6 +75,17 @@ def paged_pool(rng: np.random.Generator, g: torch.Generator, lens: np.ndarray, h
     return k_pool, v_pool, pt
 
 
+def traffic_bytes():
+    """HBM bytes per decode call measured by the committed rocprofv3 counter
+    passes (FETCH_SIZE scaled by 2, WRITE_SIZE by 1, calibrated on a 1 GiB
+    copy) for this workload, or None when that record is absent."""
+    f = ROOT / "profiles" / "decode_config2_traffic.json"
+    try:
+        return int(json.loads(f.read_text())["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def causal_flops(hq: int, hd: int, cached: np.ndarray, new: np.ndarray) -> float:
     """4 * Hq * HD * (causal-valid query/key pairs): QK^T and PV, 2 flops per MAC."""
     c = cached.astype(np.float64)
@@ -395,7 +406,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(),
+            "traffic_source": "profiles/decode_config2_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE per call)",
             "algorithmic_bytes_per_launch": int(dec_bytes),
             "avg_launch_ms": round(dec_ms, 5),
         },

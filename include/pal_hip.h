@@ -9,7 +9,9 @@
  *
  * Conventions
  *  - All tensor arguments are raw device pointers to contiguous row-major
- *    buffers allocated by the caller; the library never allocates or frees.
+ *    buffers allocated by the caller; the library never allocates or frees
+ *    device memory (pal_paged_attention creates one side stream and two
+ *    events per device on first use).
  *  - fp16 / bf16 data is passed as `void*`, with a dtype code.
  *  - `stream` is a hipStream_t passed as `void*` (NULL = the null stream).
  *    Launches are asynchronous; the caller synchronises.

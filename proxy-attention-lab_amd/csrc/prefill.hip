@@ -13,16 +13,20 @@
 //  * One workgroup (4 wavefronts) owns a tile of 128 "M-rows": QT consecutive
 //    query tokens of one sequence times the (up to 16) query heads sharing a
 //    kv head, so one K/V tile in LDS serves the whole GQA group.
-//  * Per 32-key step the workgroup stages K (as [HD/8][32][8], the page's own
-//    striped layout) and V (as [HD][32 + 4], rows of 72 bytes so the PV
-//    operand reads are free of bank conflicts) in LDS, double buffered, with
-//    the global loads of the next step held in registers during the compute
-//    (one barrier per step); then
-//    each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
+//  * Per 32-key step the K and V tiles reach LDS by direct-to-LDS copies
+//    (global_load_lds_dwordx4, no registers), issued two steps ahead into four
+//    LDS buffers, with counted waits and one barrier per step.  Page ids come
+//    from an LDS copy of the tile's page-table slice.  Steps at the tile end
+//    or with dense prompt keys take a synchronous register path.
+//  * Each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
 //    from LDS, B = Q^T held in registers) and O^T += V^T * P^T with the same
 //    instruction.  In the transposed products a lane owns one M-row, so the
-//    softmax max / sum need one cross-half exchange and the probabilities go
-//    into the PV MFMA without leaving the lane.
+//    softmax max / sum need one cross-half exchange (v_permlane32_swap) and
+//    the probabilities go into the PV MFMA without leaving the lane.  K is
+//    stored in the QK operand's row order and V rows are swizzled, so every
+//    operand read is one conflict-free 16-byte LDS access.
+//  * Steps are software-pipelined inside a wavefront: the QK MFMAs of step
+//    st+1 are issued among the exponentials of step st.
 //  * Online softmax in log2 units with a lazy rescale: the running max is only
 //    moved when a score exceeds it by more than 2^8, so O is rescaled rarely.
 //  * Causal skipping: the key loop stops at the tile's largest limit, and key
