@@ -522,16 +522,18 @@ void decode_stream_kernel(const DecodeParams p) {
 // a workgroup per slot at a time, the grid striding over the live workers.
 // A split segment (sequence, kv head, head chunk) is merged head by head, a
 // wavefront per head: M = max_c m_c, out = sum_c 2^(m_c - M) O_c /
-// sum_c 2^(m_c - M) l_c over the virtual workers c that shared it.  Lane j
-// fetches the (m, l) of the j-th contributor so those loads go out together;
-// the O loads of consecutive contributors are unrolled to keep several in
-// flight.  Workgroup 0 re-arms the claim counter.
+// sum_c 2^(m_c - M) l_c over the virtual workers c that shared it.  With up
+// to kFewParts contributors every load of the head goes out at once; beyond
+// that lane j fetches the (m, l) of the j-th contributor and the O loads of
+// consecutive contributors are unrolled.  Workgroup 0 re-arms the claim
+// counter.
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
   const int lane = lane_id();
   const int wv = wave_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
+  constexpr int kFewParts = 8;  // contributors merged with all their loads in flight
   const int64_t total = p.hdr[0];
   if (total == 0) return;
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
@@ -552,6 +554,50 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
     for (int h = wv; h < hg; h += kWorkersPerGroup) {
       const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
       auto slot_of = [&](int64_t u) { return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h; };
+
+      if (nc <= kFewParts) {
+        // the common case: every load of the head (m, l and O of each
+        // contributor) in flight at once
+        float pm[kFewParts], pl[kFewParts], po[kFewParts][kPer];
+#pragma unroll
+        for (int t = 0; t < kFewParts; ++t) {
+          if (t < nc) {
+            const int64_t sl = slot_of(v0 + t);
+            pm[t] = p.part_ml[sl * 2];
+            pl[t] = p.part_ml[sl * 2 + 1];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+              const int d = lane + q * kWave;
+              po[t][q] = d < HD ? p.part_o[sl * HD + d] : 0.f;
+            }
+          }
+        }
+        float big_m = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < kFewParts; ++t)
+          if (t < nc) big_m = fmaxf(big_m, pm[t]);
+        const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
+        float lsum = 0.f;
+        float acc[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
+#pragma unroll
+        for (int t = 0; t < kFewParts; ++t) {
+          if (t < nc) {
+            const float w = __builtin_amdgcn_exp2f(pm[t] - base_m);
+            lsum += w * pl[t];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) acc[q] += w * po[t][q];
+          }
+        }
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+          const int d = lane + q * kWave;
+          if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
+        }
+        continue;
+      }
 
       float big_m = -INFINITY;
       for (int64_t base = 0; base < nc; base += kWave) {

@@ -89,6 +89,15 @@ struct Dt<kF16> {
   }
 };
 
+// s_waitcnt immediates (gfx9 encoding): vmcnt <= n only, and lgkmcnt(0) only.
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kLgkmZero = 15 | (3 << 14) | (7 << 4);
+
+// Keeps the compiler from moving memory accesses across this point (the
+// direct-to-LDS copies and counted waits are invisible to its dependence
+// tracking).
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
 // ---------------------------------------------------------------------------
 // wave64 helpers
 // ---------------------------------------------------------------------------

@@ -51,10 +51,6 @@ constexpr int kNBuf = 4;               // LDS step buffers (read by stragglers, 
 constexpr int kPidChunk = 512;         // page ids staged per chunk; two chunks live in LDS
 constexpr float kLazyRescale = 8.f;    // log2 headroom before the running max moves
 
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding).
-constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int kLgkmZero = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0) only
-
 // A step moves 4*HD items of 16 bytes of K and as many of V.
 template <int HD>
 struct StepGeo {
@@ -394,14 +390,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   }
   __syncthreads();
   auto wait_barrier = [&](int pending_steps) {  // all but the pending_steps youngest steps' copies landed
-    asm volatile("" ::: "memory");
+    compiler_fence();
     if (pending_steps >= 1)
       __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __builtin_amdgcn_s_waitcnt(kLgkmZero);
     __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    compiler_fence();
   };
   f32x16 s_cur;
 #pragma unroll
