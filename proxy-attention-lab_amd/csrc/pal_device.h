@@ -93,6 +93,24 @@ struct Dt<kF16> {
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int kLgkmZero = 15 | (3 << 14) | (7 << 4);
 
+// Direct-to-LDS copy (global_load_lds_dwordx4): lane l copies the 16 bytes
+// at base + off to LDS byte address lds + 16 l; base and lds wave-uniform.
+// Issued as inline assembly so that the compiler does not track an LDS write
+// in flight: it would otherwise wait for every such copy (vmcnt(0)) before
+// later LDS reads it cannot prove disjoint.  Callers wait with counted
+// s_waitcnt.  The s_nop keeps the one wait state between the M0 write and
+// the copy.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));  // low half of a generic LDS address
+}
+__device__ __forceinline__ void copy_to_lds16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
+// Scheduling fence: the compiler's instruction scheduler moves nothing
+// across this point (data dependences are unaffected; waits are inserted
+// as usual).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 // Keeps the compiler from moving memory accesses across this point (the
 // direct-to-LDS copies and counted waits are invisible to its dependence
 // tracking).

@@ -37,6 +37,8 @@
 //    the dense prompt K/V rows s*P + i, as prefill.h.metal:147-234 reads
 //    them), or windows of consecutive query rows (the fused op), each run of
 //    rows of one sequence in a window being a tile.
+#include <type_traits>
+
 #include "pal_device.h"
 
 namespace pal {
@@ -114,6 +116,8 @@ struct ItemMap {
   static __device__ __forceinline__ int v_slot(int d, int kg) {
     return TPP == 16 ? (kg / 16) * (2 * HD) + d * 2 + (((kg / 8) % 2) ^ v_swz(d)) : d * 4 + ((kg / 8) ^ v_swz(d));
   }
+  // v_slot(d + 32 n, kg) - v_slot(d, kg): v_swz depends on bits 1..3 of d only
+  static constexpr int kVRowTile = TPP == 16 ? 64 : 128;
 };
 
 // One query tile: rows [row0, row0 + nrows) of sequence s (nrows <= tokens
@@ -221,7 +225,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     for (int e = chunk * kPidChunk + tid; e < min((chunk + 1) * kPidChunk, n_pid); e += kPfThreads)
       pid_lds[e % (2 * kPidChunk)] = pt[e];
   };
-  auto page_of = [&](int e) { return __builtin_amdgcn_readfirstlane(pid_lds[e % (2 * kPidChunk)]); };
 
   // Fast step: all 32 keys below the tile's largest limit, in valid pages
   // (and, in prompt mode, below the history): one direct-to-LDS copy per item,
@@ -231,37 +234,38 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // Slow step (tile end, invalid pages, dense prompt keys): register loads,
   // masked, then LDS stores -- synchronous, so it also drains the copies in
   // flight, which keeps the counted waits safe.
-  auto issue = [&](int j) {
+  // pg0 / pg1: the pages of the step's first and (TPP 16) second 16 keys.
+  constexpr bool kAllItems = NI % kPfThreads == 0;  // no wavefront has a padding copy
+  __builtin_assume(w >= 0 && w < kPfWaves);
+  // page ids >= 2^32 - 1 cannot occur with fewer pages; such an id takes the slow path
+  const uint32_t np32 = p.num_pages > 0xFFFFFFFFll ? 0xFFFFFFFFu : static_cast<uint32_t>(p.num_pages);
+  auto issue = [&](int j, uint32_t pg0, uint32_t pg1) {
     const int buf = j % kNBuf;
     const int k0 = j * kKeys;
-    const uint32_t pg0 = page_of(k0 / TPP);
-    const uint32_t pg1 = TPP == 16 ? page_of(k0 / TPP + 1) : pg0;
-    const bool fast = k0 + kKeys <= max_lim && pg0 < p.num_pages && pg1 < p.num_pages &&
-                      (!prompt_mode || k0 + kKeys <= hist);
+    if (TPP != 16) pg1 = pg0;
+    const bool fast = k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
     if (fast) {
+      const int64_t off0 = static_cast<int64_t>(pg0) * page_stride + kv_head_off;
+      const int64_t off1 = static_cast<int64_t>(pg1) * page_stride + kv_head_off;
 #pragma unroll
       for (int jj = 0; jj < NL; ++jj) {
         const int i = tid + jj * kPfThreads;
         const int ib = w * kWave + jj * kPfThreads;  // first item of this wavefront's load
-        const bool ok = ib < NI;
-        const uint32_t pg = IM::k_page_half(ok ? ib : 0) ? pg1 : pg0;
-        const uint16_t* page = p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off;
-        const uint16_t* src = page + (ok ? IM::k_offset(i) : 0);
-        uint16_t* dst = ok ? k_lds(buf) + ib * 8 : junk_lds;
-        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+        const bool ok = kAllItems || ib < NI;
+        const uint16_t* page = p.k_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
+        const uint32_t src = 2u * static_cast<uint32_t>(ok ? IM::k_offset(i) : 0);
+        copy_to_lds16(page, src, lds_addr(ok ? k_lds(buf) + ib * 8 : junk_lds));
       }
 #pragma unroll
       for (int jj = 0; jj < NL; ++jj) {
         const int i = tid + jj * kPfThreads;
         const int ib = w * kWave + jj * kPfThreads;
-        const bool ok = ib < NI;
-        const uint32_t pg = IM::k_page_half(ok ? ib : 0) ? pg1 : pg0;
-        const uint16_t* page = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off;
+        const bool ok = kAllItems || ib < NI;
+        const uint16_t* page = p.v_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
         int d = 0, key = 0;
         if (ok) IM::v_item(i, d, key);
-        const uint16_t* src = page + d * TPP + key % TPP;
-        uint16_t* dst = ok ? v_lds(buf) + ib * 8 : junk_lds;
-        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+        const uint32_t src = 2u * static_cast<uint32_t>(d * TPP + key % TPP);
+        copy_to_lds16(page, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
       }
       return;
     }
@@ -323,6 +327,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       }
     }
   };
+  // the page ids of step j (an LDS broadcast read; TPP 32: one page)
+  auto read_pids = [&](int j) {
+    const int e = (j * kKeys / TPP) % (2 * kPidChunk);
+    u32x2 v;
+    if (TPP == 16) {
+      v = *reinterpret_cast<const u32x2*>(pid_lds + e);  // e is even: 8-byte aligned
+    } else {
+      v.x = pid_lds[e];
+      v.y = v.x;
+    }
+    return v;
+  };
 
   float m_run = -INFINITY;  // running max of this lane's M-row (raw score units)
   float l_run = 0.f;        // this lane's share of the exp-sum
@@ -346,23 +362,20 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       ka[kk] = *reinterpret_cast<const u32x4*>(k_lds(buf) + IM::k_slot(col, c) * 8);
     }
   };
+  // V^T operand bases: k-step kk takes keys 16kk + 8 half .. +7; row tile n
+  // (dims 32n + col) sits kVRowTile slots further
+  const int v_base[2] = {IM::v_slot(col, 8 * half), IM::v_slot(col, 16 + 8 * half)};
   // register r holds key k0 + 16 (r/8) + 8 half + 4 ((r/4)%2) + r%4 of
   // M-row col.  Scores stay raw (the scale is positive, so maxima commute
   // with it); the exponent is one fma: s * scale_log2 - m * scale_log2.
-  // Masks the step's scores, moves the running max if needed (lazily) and
-  // returns the exponent offset.
-  auto mask_and_max = [&](f32x16& sacc, int st) {
-    const int k0 = st * kKeys;
-    float bm = -INFINITY;
-    if (k0 + kKeys > min_lim) {  // some key of this step is masked for some row
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
-        if (key >= my_lim) sacc[r] = -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sacc[r]);
+  auto mask_score = [&](f32x16& sacc, int r, int st) {
+    const int key = st * kKeys + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+    if (key >= my_lim) sacc[r] = -INFINITY;
+  };
+  // Given this lane's max bm of a step's scores: moves the running max to the
+  // row max if it grew by more than the headroom (rescaling this row's O and
+  // exp-sum), and returns the exponent offset of the step.
+  auto update_max = [&](float bm) {
     bm = max_xor32(bm);
     if (__ballot(bm > m_run + kLazyRescale * p.scale_inv_log2)) {
       const bool grow = bm > m_run + kLazyRescale * p.scale_inv_log2;
@@ -378,12 +391,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     return (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
   };
 
-  // Pipeline.  Memory: steps st+1 and st+2 are in flight (direct-to-LDS)
-  // while step st is computed; four buffers, because a straggling wavefront
-  // may still read steps st and st+1 when the copies of step st+2 start.
-  // Compute: inside a wavefront, the QK MFMAs of step st+1 are interleaved
-  // with the exponentials of step st (independent work for the matrix and
-  // vector units), then the PV MFMAs of step st follow.
+  // Pipeline.  Memory: three steps ahead.  Iteration st waits for step st+1
+  // (step st+2 may still be in flight), passes the barrier, and then issues
+  // the copies of step st+3 into the buffer of step st-1, which every
+  // wavefront finished reading before the barrier; hence four buffers.
+  // Compute, inside a wavefront: all operand reads of the iteration go out
+  // first; the QK MFMAs of step st+1 run beside the exponentials of step st,
+  // and the PV MFMAs of step st beside the exp-sum of step st and the row max
+  // of step st+1, which gives the next iteration its exponent offset.
   if (nsteps > 0) {
     stage_pids(0);
     if (n_pid > kPidChunk) stage_pids(1);
@@ -391,7 +406,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   __syncthreads();
   auto wait_barrier = [&](int pending_steps) {  // all but the pending_steps youngest steps' copies landed
     compiler_fence();
-    if (pending_steps >= 1)
+    if (pending_steps >= 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NL));
+    else if (pending_steps == 1)
       __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
@@ -402,68 +419,92 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   f32x16 s_cur;
 #pragma unroll
   for (int r = 0; r < 16; ++r) s_cur[r] = 0.f;
+  float mb = 0.f;
   if (nsteps > 0) {
-    issue(0);
-    if (nsteps > 1) issue(1);
-    wait_barrier(nsteps > 1 ? 1 : 0);
+    for (int j = 0; j < 3 && j < nsteps; ++j) {
+      const u32x2 pg = read_pids(j);
+      issue(j, __builtin_amdgcn_readfirstlane(pg.x), __builtin_amdgcn_readfirstlane(pg.y));
+    }
+    wait_barrier(min(nsteps - 1, 2));  // step 0 has landed
     u32x4 ka[KS];
     read_k(0, ka);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) s_cur = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_cur);
-  }
-  for (int st = 0; st < nsteps; ++st) {
-    const int j = st + 2;
-    if (j < nsteps) {
-      // entering page-id chunk q (q >= 1): stage chunk q + 1 over chunk q - 1,
-      // whose last reader was at least one barrier ago
-      const int e0 = j * kKeys / TPP;
-      if (e0 % kPidChunk == 0 && e0 > 0 && e0 + kPidChunk < n_pid) {
-        stage_pids(e0 / kPidChunk + 1);
-        __syncthreads();
-      }
-      issue(j);
+    float bm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (min_lim < kKeys) mask_score(s_cur, r, 0);
+      bm = fmaxf(bm, s_cur[r]);
     }
-    wait_barrier(j < nsteps ? 1 : 0);  // step st+1 has landed
-
-    const float mb = mask_and_max(s_cur, st);
-    // (on the last step the "next" QK reads a stale, in-bounds buffer and its
-    // result is dropped: one extra QK per tile keeps the region branch-free)
+    mb = update_max(bm);
+  }
+  // Steps whose next step needs no mask (every row sees all its keys) run
+  // the unmasked body.  The last step is always in the masked part, whose
+  // mask also discards the scores of the stale buffer it reads as "next".
+  const int n_main = max(0, min(nsteps, min_lim / kKeys - 1));
+  auto step = [&](auto masked, int st) {
+    constexpr bool kMask = decltype(masked)::value;
+    wait_barrier(st + 2 < nsteps ? 1 : 0);  // step st+1 has landed
+    const int j = st + 3;
+    const u32x2 pgv = read_pids(j);  // used after the MFMAs (in bounds whether or not step j exists)
     u32x4 ka[KS];
     read_k(st + 1, ka);
-    u32x4 va[2][DT32];
-    {
-      const int buf = st % kNBuf;
+    float pe[16];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int n = 0; n < DT32; ++n)
-          va[kk][n] = *reinterpret_cast<const u32x4*>(v_lds(buf) + IM::v_slot(32 * n + col, 16 * kk + 8 * half) * 8);
-    }
-    // QK of step st+1 (matrix unit) alongside the exponentials of step st
+    for (int r = 0; r < 16; ++r) pe[r] = fmaf(s_cur[r], p.scale_log2, mb);
+    // The rest is written in issue order, chunk by chunk, with scheduling
+    // fences between chunks (the compiler would otherwise keep two operand
+    // reads in flight, wait before every MFMA and bunch the vector work):
+    // each QK MFMA of step st+1 (K operands all read above) goes out with one
+    // V operand read of step st and a share of step st's exponentials and
+    // conversions; each PV MFMA of step st with a share of the exp-sum and of
+    // the row max of step st+1.
+    sched_fence();
+    const int vbuf = st % kNBuf;
     f32x16 s_next;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
+    u32x4 va[KS];  // PV operand m: k-step m / DT32, row tile m % DT32 (KS == 2 * DT32)
+    uint32_t pp[8];  // packed probabilities of the lane's scores 2q, 2q+1
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) s_next = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_next);
-    float pe[16];
+    for (int kk = 0; kk < KS; ++kk) {
+      s_next = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_next);
+      va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      pe[r] = __builtin_amdgcn_exp2f(fmaf(s_cur[r], p.scale_log2, mb));
-      l_run += pe[r];
+      for (int r = kk * 16 / KS; r < (kk + 1) * 16 / KS; ++r) pe[r] = __builtin_amdgcn_exp2f(pe[r]);
+#pragma unroll
+      for (int q = kk * 8 / KS; q < (kk + 1) * 8 / KS; ++q) pp[q] = Dt<DT>::pack2(pe[2 * q], pe[2 * q + 1]);
+      sched_fence();
     }
-    u32x4 pb[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-      pb[kk] = u32x4{Dt<DT>::pack2(pe[8 * kk + 0], pe[8 * kk + 1]), Dt<DT>::pack2(pe[8 * kk + 2], pe[8 * kk + 3]),
-                     Dt<DT>::pack2(pe[8 * kk + 4], pe[8 * kk + 5]), Dt<DT>::pack2(pe[8 * kk + 6], pe[8 * kk + 7])};
+    const u32x4 pb[2] = {u32x4{pp[0], pp[1], pp[2], pp[3]}, u32x4{pp[4], pp[5], pp[6], pp[7]}};
     // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
     // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
+    float bm = -INFINITY;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int m = 0; m < KS; ++m) {
+      o[m % DT32] = Dt<DT>::mma32x32x16(va[m], pb[m / DT32], o[m % DT32]);
 #pragma unroll
-      for (int n = 0; n < DT32; ++n) o[n] = Dt<DT>::mma32x32x16(va[kk][n], pb[kk], o[n]);
+      for (int r = m * 16 / KS; r < (m + 1) * 16 / KS; ++r) {
+        l_run += pe[r];
+        if (kMask) mask_score(s_next, r, st + 1);
+        bm = fmaxf(bm, s_next[r]);
+      }
+      sched_fence();
+    }
+    mb = update_max(bm);
+    if (j < nsteps) {
+      // entering page-id chunk q (q >= 1): stage chunk q + 1 over chunk q - 1,
+      // whose last reader finished before this iteration's barrier; the next
+      // barriers publish it long before its first reader
+      const int e0 = j * kKeys / TPP;
+      if (e0 % kPidChunk == 0 && e0 > 0 && e0 + kPidChunk < n_pid) stage_pids(e0 / kPidChunk + 1);
+      issue(j, __builtin_amdgcn_readfirstlane(pgv.x), __builtin_amdgcn_readfirstlane(pgv.y));
+    }
     s_cur = s_next;
-  }
+  };
+  int st = 0;
+  for (; st < n_main; ++st) step(std::false_type{}, st);
+  for (; st < nsteps; ++st) step(std::true_type{}, st);
 
   // ---- normalise and write: lane holds O[M-row col][32n + 8(r/4) + 4 half + r%4]
   float l = sum_xor32(l_run);
