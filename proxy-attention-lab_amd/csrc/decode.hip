@@ -227,9 +227,6 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   constexpr int NT = HD / 16;            // output tiles of 16 dims
   constexpr int PF = PAL_DECODE_PREFETCH;
   constexpr int NBUF = PF + 1;
-  // Blocks whose page ids one vector load (one id per lane) always covers,
-  // whatever the alignment of the first block within its page.
-  constexpr int kChunkBlocks = (kWave - 1) * TPP / 16;
 
   const int64_t b0 = vstart(sc, v);
   int64_t remaining = vstart(sc, v + 1) - b0;
@@ -298,13 +295,26 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t c0 = 0; c0 < count; c0 += kChunkBlocks) {
-      const int n_blk = static_cast<int>((count - c0) < kChunkBlocks ? (count - c0) : kChunkBlocks);
-      const int64_t bstart = blk + c0;            // first block of this chunk
+    {
+      // Page ids in register windows of 64 pages (one id per lane): pid_cur
+      // holds window wcur, the window of the block being computed, and
+      // pid_nxt window wcur+1 (the loads run at most a few blocks ahead).
+      // Every step group also loads window wcur+2 (unconditionally, so the
+      // vector-memory stream of the loop is the same every time and the
+      // compiler's counted waits stay exact); when the computed block
+      // enters window wcur+1 the windows move up by one, taking the window
+      // wcur+2 loaded a step group earlier.  The K/V pipeline never stops for
+      // page ids inside a piece.
+      const int64_t n_blk = count;
+      const int64_t bstart = blk;                 // first block of the piece
       const int64_t pbase = (bstart * 16) / TPP;  // its page index
-      int64_t lp = pbase + lane;
-      if (lp >= p.page_table_width) lp = p.page_table_width - 1;
-      const uint32_t pid = pt[lp];
+      auto load_window = [&](int64_t wi) {
+        int64_t lp = pbase + wi * kWave + lane;
+        if (lp >= p.page_table_width) lp = p.page_table_width - 1;
+        return pt[lp];
+      };
+      int64_t wcur = 0;
+      uint32_t pid_cur = load_window(0), pid_nxt = load_window(1), pid_later = load_window(2);
 
       u32x4 kb4[NBUF][kK32 ? KK : 1];
       u32x2 kb2[NBUF][kK32 ? 1 : KK];
@@ -314,9 +324,10 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       // Issue the K and V loads of chunk block i into buffer `buf`.  An
       // out-of-range page id is replaced by page 0 (in bounds) and the block
       // is masked out when computed.
-      auto issue = [&](int i, int buf) {
+      auto issue = [&](int64_t i, int buf) {
         const int64_t b = bstart + i;
-        const uint32_t pg = __builtin_amdgcn_readlane(pid, static_cast<int>((b * 16) / TPP - pbase));
+        const int64_t e = (b * 16) / TPP - pbase;  // page of the piece
+        const uint32_t pg = __builtin_amdgcn_readlane((e >> 6) == wcur ? pid_cur : pid_nxt, static_cast<int>(e & 63));
         bv[buf] = pg < p.num_pages;
         const uint32_t page = bv[buf] ? pg : 0u;
         const int slot0 = static_cast<int>((b * 16) % TPP);
@@ -336,7 +347,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
         for (int n = 0; n < NT; ++n) vb[buf][n] = *reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP);
       };
 
-      auto compute = [&](int i, int buf) {
+      auto compute = [&](int64_t i, int buf) {
         const int64_t b = bstart + i;
         const bool live = bv[buf] && i < n_blk;  // steps past the chunk end are fully masked
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -393,13 +404,22 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       // PF blocks in flight are never drained early.
 #pragma unroll
       for (int q = 0; q < PF; ++q) issue(q < n_blk ? q : n_blk - 1, q);
-      for (int i0 = 0; i0 < n_blk; i0 += NBUF) {
+      for (int64_t i0 = 0; i0 < n_blk; i0 += NBUF) {
+        const uint32_t pid_ahead = load_window(wcur + 2);
 #pragma unroll
         for (int u = 0; u < NBUF; ++u) {
-          const int i = i0 + u;
+          const int64_t i = i0 + u;
           issue(i + PF < n_blk ? i + PF : n_blk - 1, (u + PF) % NBUF);
           compute(i, u);
         }
+        // entered window wcur+1: move the windows up (at most NBUF + PF pages
+        // past its start, so no issue has needed window wcur+2 yet)
+        const int64_t e_last = ((bstart + i0 + NBUF - 1) * 16) / TPP - pbase;
+        const bool up = (e_last >> 6) > wcur;
+        pid_cur = up ? pid_nxt : pid_cur;
+        pid_nxt = up ? pid_later : pid_nxt;
+        wcur += up ? 1 : 0;
+        pid_later = pid_ahead;
       }
     }
 
