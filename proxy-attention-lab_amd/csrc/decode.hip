@@ -212,20 +212,14 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   }
 }
 
-#ifdef PAL_DECODE_WAVES_PER_EU
-#define PAL_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(PAL_DECODE_WAVES_PER_EU, PAL_DECODE_WAVES_PER_EU)))
-#else
-#define PAL_DECODE_OCCUPANCY
-#endif
-
-// Streams the blocks of virtual worker v (one wavefront).
-template <int DT, int HD, int TPP>
+// Streams the blocks of virtual worker v (one wavefront), with the loads of
+// PF blocks in flight ahead of the one being computed.
+template <int DT, int HD, int TPP, int PF>
 __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched& sc, const int64_t* cum,
                                               int64_t n_items, int64_t v) {
   constexpr bool kK32 = (HD % 32) == 0;  // QK k-step of 32 (else 16)
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
   constexpr int NT = HD / 16;            // output tiles of 16 dims
-  constexpr int PF = PAL_DECODE_PREFETCH;
   constexpr int NBUF = PF + 1;
 
   const int64_t b0 = vstart(sc, v);
@@ -321,9 +315,12 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       u32x2 vb[NBUF][NT];
       bool bv[NBUF];
 
-      // Issue the K and V loads of chunk block i into buffer `buf`.  An
-      // out-of-range page id is replaced by page 0 (in bounds) and the block
-      // is masked out when computed.
+      // Issue the K and V loads of block i of the piece into buffer `buf`.
+      // An out-of-range page id is replaced by page 0 (in bounds) and the
+      // block is masked out when computed.  Every K/V block is read exactly
+      // once per call, so the loads carry the non-temporal hint: the stream
+      // does not displace other lines (page ids, partials, the fused op's
+      // prefill tiles) from L2 and MALL.
       auto issue = [&](int64_t i, int buf) {
         const int64_t b = bstart + i;
         const int64_t e = (b * 16) / TPP - pbase;  // page of the piece
@@ -337,14 +334,16 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
         for (int kk = 0; kk < KK; ++kk) {
           if constexpr (kK32) {
             const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
-            kb4[buf][kk] = *reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8);
+            kb4[buf][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8));
           } else {
             const int d = 16 * kk + 4 * g;  // dims d .. d+3
-            kb2[buf][kk] = *reinterpret_cast<const u32x2*>(kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7));
+            kb2[buf][kk] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x2*>(kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7)));
           }
         }
 #pragma unroll
-        for (int n = 0; n < NT; ++n) vb[buf][n] = *reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP);
+        for (int n = 0; n < NT; ++n)
+          vb[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP));
       };
 
       auto compute = [&](int64_t i, int buf) {
@@ -474,11 +473,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   }
 }
 
-template <int DT, int HD, int TPP>
-__global__ __launch_bounds__(kGroupThreads) PAL_DECODE_OCCUPANCY
-void decode_stream_kernel(const DecodeParams p) {
-  __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
-  __shared__ int64_t wave_sums[kWorkersPerGroup];
+template <int DT, int HD, int TPP, int PF>
+__device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_lds, int64_t* wave_sums) {
   const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
   const int64_t* cum = p.cum;
   int64_t total = 0;
@@ -525,14 +521,44 @@ void decode_stream_kernel(const DecodeParams p) {
   if (total == 0) return;
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
   const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (w < sc.nws) process_range<DT, HD, TPP>(p, sc, cum, n_items, w);
+  if (w < sc.nws) process_range<DT, HD, TPP, PF>(p, sc, cum, n_items, w);
   while (sc.nc > 0) {
     uint32_t k = 0;
     if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
     k = __builtin_amdgcn_readfirstlane(k);
     if (k >= sc.nc) break;
-    process_range<DT, HD, TPP>(p, sc, cum, n_items, sc.nws + k);
+    process_range<DT, HD, TPP, PF>(p, sc, cum, n_items, sc.nws + k);
   }
+}
+
+// Plain decode: the whole GPU streams KV, one wavefront per SIMD with the
+// deepest prefetch the register file allows.
+template <int DT, int HD, int TPP>
+__global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const DecodeParams p) {
+  __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
+  __shared__ int64_t wave_sums[kWorkersPerGroup];
+  stream_body<DT, HD, TPP, PAL_DECODE_PREFETCH>(p, cum_lds, wave_sums);
+}
+
+// Decode rows of the fused op: one workgroup per CU, held to half of the
+// register file (for head_dim 128 with a shallower prefetch) so that a
+// prefill tile wavefront fits on every SIMD beside it and the HBM-bound
+// decode overlaps the MFMA-bound prefill instead of taking turns with it.
+// Head dims above 128 use decode_stream_kernel: their prefill tiles need
+// more than half of the register file themselves.
+constexpr bool shares_cu(int hd) { return hd <= 128; }
+
+template <int HD, int TPP>
+constexpr int shared_cu_prefetch() {
+  return HD <= 96 ? PAL_DECODE_PREFETCH : (TPP == 16 ? PAL_DECODE_PREFETCH - 1 : PAL_DECODE_PREFETCH - 2);
+}
+
+template <int DT, int HD, int TPP>
+__global__ __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_shared_cu_kernel(const DecodeParams p) {
+  __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
+  __shared__ int64_t wave_sums[kWorkersPerGroup];
+  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>()>(p, cum_lds, wave_sums);
 }
 
 // Walks the merge list, slot v for virtual worker v (first block < 0:
@@ -665,7 +691,7 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
 }
 
 template <int DT, int HD, int TPP>
-hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t stream) {
   hipError_t err;
   if (p.num_seqs > kInlinePlanSeqs) {
     hipLaunchKernelGGL((decode_plan_kernel<HD, TPP>), dim3(1), dim3(kPlanThreads), 0, stream, p);
@@ -673,8 +699,17 @@ hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     if (err != hipSuccess) return err;
   }
   const int64_t groups = (static_cast<int64_t>(p.num_workers) + kWorkersPerGroup - 1) / kWorkersPerGroup;
-  hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)), dim3(kGroupThreads),
-                     0, stream, p);
+  bool plain = true;
+  if constexpr (shares_cu(HD)) {
+    if (shared_cu) {
+      hipLaunchKernelGGL((decode_shared_cu_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)),
+                         dim3(kGroupThreads), 0, stream, p);
+      plain = false;
+    }
+  }
+  if (plain)
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)),
+                       dim3(kGroupThreads), 0, stream, p);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int64_t merge_groups = p.list_cap < kMergeGroups ? p.list_cap : kMergeGroups;
@@ -684,23 +719,23 @@ hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
 }
 
 template <int DT, int HD>
-hipError_t dispatch_tpp(const DecodeParams& p, int tpp, hipStream_t stream) {
+hipError_t dispatch_tpp(const DecodeParams& p, int tpp, bool shared_cu, hipStream_t stream) {
   switch (tpp) {
-    case 16: return launch_decode_t<DT, HD, 16>(p, stream);
-    case 32: return launch_decode_t<DT, HD, 32>(p, stream);
+    case 16: return launch_decode_t<DT, HD, 16>(p, shared_cu, stream);
+    case 32: return launch_decode_t<DT, HD, 32>(p, shared_cu, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int DT>
-hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, hipStream_t stream) {
+hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, bool shared_cu, hipStream_t stream) {
   switch (hd) {
-    case 32: return dispatch_tpp<DT, 32>(p, tpp, stream);
-    case 64: return dispatch_tpp<DT, 64>(p, tpp, stream);
-    case 80: return dispatch_tpp<DT, 80>(p, tpp, stream);
-    case 96: return dispatch_tpp<DT, 96>(p, tpp, stream);
-    case 128: return dispatch_tpp<DT, 128>(p, tpp, stream);
-    case 256: return dispatch_tpp<DT, 256>(p, tpp, stream);
+    case 32: return dispatch_tpp<DT, 32>(p, tpp, shared_cu, stream);
+    case 64: return dispatch_tpp<DT, 64>(p, tpp, shared_cu, stream);
+    case 80: return dispatch_tpp<DT, 80>(p, tpp, shared_cu, stream);
+    case 96: return dispatch_tpp<DT, 96>(p, tpp, shared_cu, stream);
+    case 128: return dispatch_tpp<DT, 128>(p, tpp, shared_cu, stream);
+    case 256: return dispatch_tpp<DT, 256>(p, tpp, shared_cu, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -726,13 +761,17 @@ const void* stream_kernel_for(int hd, int tpp) {
 
 }  // namespace
 
-hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, int* workers) {
+hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, int* workers) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
   int cus = 0;
   err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (err != hipSuccess) return err;
+  if (shared_cu && shares_cu(head_dim)) {  // one workgroup per CU; the prefill tiles take the rest
+    *workers = cus * kWorkersPerGroup;
+    return hipSuccess;
+  }
   const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page)
                                   : stream_kernel_for<kF16>(head_dim, tokens_per_page);
   if (!fn) return hipErrorInvalidValue;
@@ -744,9 +783,10 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
   return hipSuccess;
 }
 
-hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream) {
-  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, stream);
-  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, stream);
+hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
+                         hipStream_t stream) {
+  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, shared_cu, stream);
+  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, shared_cu, stream);
 }
 
 }  // namespace pal

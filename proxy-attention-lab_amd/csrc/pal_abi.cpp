@@ -94,10 +94,10 @@ DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t v
 // per worker, or, with a partition size, one chunk per partition of the
 // page-table capacity.
 int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seqs, int num_kv_heads,
-                   int head_chunks, int64_t page_table_width, int partition_size, int* resident,
+                   int head_chunks, int64_t page_table_width, int partition_size, bool shared_cu, int* resident,
                    int64_t* virtual_workers) {
   int res = 0;
-  hipError_t err = pal::decode_resident_workers(dtype, head_dim, tokens_per_page, &res);
+  hipError_t err = pal::decode_resident_workers(dtype, head_dim, tokens_per_page, shared_cu, &res);
   if (err != hipSuccess)
     return fail(PAL_ERR_HIP, "[paged_attention_decode] occupancy query failed: %s", hipGetErrorString(err));
   int64_t vw;
@@ -279,7 +279,7 @@ size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, in
   int resident = 0;
   int64_t vw = 0;
   if (decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                     partition_size, &resident, &vw) != PAL_OK)
+                     partition_size, false, &resident, &vw) != PAL_OK)
     return 0;
   return decode_layout(num_seqs, head_dim, group < 16 ? group : 16, vw).total;
 }
@@ -323,7 +323,7 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
   int resident = 0;
   int64_t vw = 0;
   const int st = decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                                partition_size, &resident, &vw);
+                                partition_size, false, &resident, &vw);
   if (st != PAL_OK) return st;
   const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, vw);
   if (workspace == nullptr || workspace_bytes < lay.total)
@@ -336,7 +336,7 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                             static_cast<char*>(workspace), lay, num_seqs, num_pages,
                                             page_table_width, num_q_heads, num_kv_heads, head_dim, resident,
                                             partition_size);
-  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)),
+  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, false, static_cast<hipStream_t>(stream)),
                     "paged_attention_decode");
 }
 
@@ -407,7 +407,7 @@ size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int
   int resident = 0;
   int64_t vw = 0;
   if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
-                     &resident, &vw) != PAL_OK)
+                     true, &resident, &vw) != PAL_OK)
     return 0;
   return decode_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
 }
@@ -439,7 +439,8 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   const int chunks = (group + 15) / 16;
   int resident = 0;
   int64_t vw = 0;
-  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, &resident, &vw);
+  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, true, &resident,
+                      &vw);
   if (st != PAL_OK) return st;
   const DecodeLayout lay = decode_layout(num_query_rows, head_dim, hg_max, vw);
   if (workspace == nullptr || workspace_bytes < lay.total)
@@ -500,7 +501,7 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   if (err != hipSuccess) return hip_status(err, op);
   err = hipStreamWaitEvent(ss->stream, ss->fork, 0);
   if (err != hipSuccess) return hip_status(err, op);
-  err = pal::launch_decode(dp, dtype, head_dim, tokens_per_page, hs);
+  err = pal::launch_decode(dp, dtype, head_dim, tokens_per_page, true, hs);
   if (err != hipSuccess) return hip_status(err, op);
   err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, ss->stream);
   if (err != hipSuccess) return hip_status(err, op);

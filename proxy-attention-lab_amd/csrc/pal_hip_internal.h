@@ -71,9 +71,11 @@ struct DecodeParams {
   float scale_log2;       // log2(e) / sqrt(HD)
 };
 
-// Workers the GPU keeps resident for this kernel configuration.
-hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, int* workers);
-hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
+// Workers the GPU keeps resident for this kernel configuration (shared_cu:
+// the fused op's decode, one workgroup per CU beside the prefill tiles).
+hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, int* workers);
+hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
+                         hipStream_t stream);
 
 // Causal attention over query tiles (prefill rows).  Uniform-prompt mode
 // (prompt_len > 0): the reference prefill, keys past each sequence's history
