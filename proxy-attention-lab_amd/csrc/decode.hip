@@ -1,7 +1,7 @@
 // Paged-attention decode for gfx950: the KV stream of the whole batch is split
 // into 16-token blocks, shared out to a resident set of wavefront workers
-// (three quarters statically, the rest claimed dynamically in small chunks),
-// and the pieces of sequences that several workers shared are merged with a
+// (equal static shares, or fixed chunks claimed from a counter when a
+// partition size is given), and the pieces of sequences that several workers shared are merged with a
 // log-sum-exp pass.
 //
 // Reference behaviour: kernels/paged_attention/decode/paged_attention_decode.h.metal
@@ -46,15 +46,12 @@
 //    merge grid does not grow with the batch.
 #include "pal_device.h"
 
-#ifndef PAL_DECODE_PREFETCH
-#define PAL_DECODE_PREFETCH 3  // blocks whose loads are in flight ahead of the one being computed
-#endif
-
 namespace pal {
 
 namespace {
 
 constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
+constexpr int kPrefetch = 2;         // blocks whose loads are in flight ahead of the one being computed
 constexpr int kGroupThreads = kWorkersPerGroup * kWave;
 constexpr int kPlanThreads = 1024;
 constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each workgroup
@@ -531,26 +528,28 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
   }
 }
 
-// Plain decode: the whole GPU streams KV, one wavefront per SIMD with the
-// deepest prefetch the register file allows.
+// Plain decode: the whole GPU streams KV, one wavefront per SIMD.  (With
+// the non-temporal loads a third block of prefetch, or two wavefronts per
+// SIMD, measured slower.)
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const DecodeParams p) {
   __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, PAL_DECODE_PREFETCH>(p, cum_lds, wave_sums);
+  stream_body<DT, HD, TPP, kPrefetch>(p, cum_lds, wave_sums);
 }
 
 // Decode rows of the fused op: one workgroup per CU, held to half of the
-// register file (for head_dim 128 with a shallower prefetch) so that a
-// prefill tile wavefront fits on every SIMD beside it and the HBM-bound
-// decode overlaps the MFMA-bound prefill instead of taking turns with it.
+// register file (head_dim 128 with 32-token pages: one block of prefetch)
+// so that a prefill tile wavefront fits on every SIMD beside it and the
+// HBM-bound decode overlaps the MFMA-bound prefill instead of taking turns
+// with it.
 // Head dims above 128 use decode_stream_kernel: their prefill tiles need
 // more than half of the register file themselves.
 constexpr bool shares_cu(int hd) { return hd <= 128; }
 
 template <int HD, int TPP>
 constexpr int shared_cu_prefetch() {
-  return HD <= 96 ? PAL_DECODE_PREFETCH : (TPP == 16 ? PAL_DECODE_PREFETCH - 1 : PAL_DECODE_PREFETCH - 2);
+  return HD == 128 && TPP == 32 ? kPrefetch - 1 : kPrefetch;
 }
 
 template <int DT, int HD, int TPP>
