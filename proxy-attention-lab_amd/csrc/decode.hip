@@ -563,129 +563,167 @@ void decode_shared_cu_kernel(const DecodeParams p) {
 // Walks the merge list, slot v for virtual worker v (first block < 0:
 // nothing to merge; every slot of the live range was written by this call's
 // workers, with the segment's first block, block count, output row and
-// segment index, so the merge needs no other lookup);
-// a workgroup per slot at a time, the grid striding over the live workers.
-// A split segment (sequence, kv head, head chunk) is merged head by head, a
-// wavefront per head: M = max_c m_c, out = sum_c 2^(m_c - M) O_c /
-// sum_c 2^(m_c - M) l_c over the virtual workers c that shared it.  With up
-// to kFewParts contributors every load of the head goes out at once; beyond
-// that lane j fetches the (m, l) of the j-th contributor and the O loads of
-// consecutive contributors are unrolled.  Workgroup 0 re-arms the claim
-// counter.
+// segment index, so the merge needs no other lookup); a workgroup per slot
+// at a time, the grid striding over the live workers.  A split segment
+// (sequence, kv head, head chunk) is merged head by head, a wavefront per
+// head: M = max_c m_c, out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c
+// over the virtual workers c that shared it.
+//
+// The worker that wrote slot v holds the segment's first piece, so the
+// contributors are v, v+1, ...: the list slot, the header and the partials of
+// the first kSpec contributors (both partial slots of v, whose piece may be
+// its first or its last, and the first-piece slot of the others) are all
+// fetched in one round trip, before the slot says how many there are.  A
+// segment with more contributors is finished by the general loop: lane j
+// fetches the (m, l) of the j-th contributor and the O loads of consecutive
+// contributors are unrolled.  Workgroup 0 re-arms the claim counter.
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
   const int lane = lane_id();
   const int wv = wave_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
-  constexpr int kFewParts = 8;  // contributors merged with all their loads in flight
-  const int64_t total = p.hdr[0];
-  if (total == 0) return;
-  const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
-  const int64_t n_slots = sc.nws + sc.nc < p.list_cap ? sc.nws + sc.nc : p.list_cap;
-  for (int64_t e = blockIdx.x; e < n_slots; e += gridDim.x) {
+  constexpr int kSpec = 4;                              // contributors fetched with the slot
+  constexpr int kHpw = 16 / kWorkersPerGroup;           // heads per wavefront (hg_max <= 16)
+  const int64_t last_w = p.list_cap - 1;                // partial slots exist for workers < list_cap
+
+  int64_t sg0 = 0, snb = 0, srow = 0, sseg = 0;
+  float pm[kHpw][kSpec + 1], pl[kHpw][kSpec + 1], po[kHpw][kSpec + 1][kPer];
+  // index t: 0 = slot 0 of worker e, 1 = slot 1 of worker e, t >= 2 = slot 0 of worker e + t - 1
+  auto fetch = [&](int64_t e) {
     const int64_t* slot = p.split_list + 4 * e;
-    const int64_t g0 = slot[0];
-    if (g0 < 0) continue;
-    const int64_t nb = slot[1];
-    const int64_t out_row = slot[2];
-    const int seg = static_cast<int>(slot[3]);
-    const int kvh = seg / p.head_chunks;
-    const int h0 = (seg % p.head_chunks) * 16;
-    const int hg = min(16, p.group - h0);
-    const int64_t v0 = vworker_of(sc, g0);
-    const int64_t v1 = vworker_of(sc, g0 + nb - 1);
-    const int64_t nc = v1 - v0 + 1;
-    for (int h = wv; h < hg; h += kWorkersPerGroup) {
-      const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
-      auto slot_of = [&](int64_t u) { return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h; };
-
-      if (nc <= kFewParts) {
-        // the common case: every load of the head (m, l and O of each
-        // contributor) in flight at once
-        float pm[kFewParts], pl[kFewParts], po[kFewParts][kPer];
+    sg0 = slot[0];
+    snb = slot[1];
+    srow = slot[2];
+    sseg = slot[3];
 #pragma unroll
-        for (int t = 0; t < kFewParts; ++t) {
-          if (t < nc) {
-            const int64_t sl = slot_of(v0 + t);
-            pm[t] = p.part_ml[sl * 2];
-            pl[t] = p.part_ml[sl * 2 + 1];
+    for (int j = 0; j < kHpw; ++j) {
+      const int h = wv + kWorkersPerGroup * j;
+      if (h < p.hg_max) {
 #pragma unroll
-            for (int q = 0; q < kPer; ++q) {
-              const int d = lane + q * kWave;
-              po[t][q] = d < HD ? p.part_o[sl * HD + d] : 0.f;
-            }
-          }
-        }
-        float big_m = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < kFewParts; ++t)
-          if (t < nc) big_m = fmaxf(big_m, pm[t]);
-        const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
-        float lsum = 0.f;
-        float acc[kPer];
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
-#pragma unroll
-        for (int t = 0; t < kFewParts; ++t) {
-          if (t < nc) {
-            const float w = __builtin_amdgcn_exp2f(pm[t] - base_m);
-            lsum += w * pl[t];
-#pragma unroll
-            for (int q = 0; q < kPer; ++q) acc[q] += w * po[t][q];
-          }
-        }
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-          const int d = lane + q * kWave;
-          if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
-        }
-        continue;
-      }
-
-      float big_m = -INFINITY;
-      for (int64_t base = 0; base < nc; base += kWave) {
-        const int64_t j = base + lane;
-        const float m = j < nc ? p.part_ml[slot_of(v0 + j) * 2] : -INFINITY;
-        big_m = fmaxf(big_m, m);
-      }
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) big_m = fmaxf(big_m, shfl_xor(big_m, off));
-      const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
-
-      float lsum = 0.f;
-      float acc[kPer];
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
-      for (int64_t base = 0; base < nc; base += kWave) {
-        const int64_t j = base + lane;
-        float wgt = 0.f;
-        if (j < nc) {
-          const int64_t sl = slot_of(v0 + j);
-          wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
-          lsum += wgt * p.part_ml[sl * 2 + 1];
-        }
-        const int cnt = static_cast<int>((nc - base) < kWave ? (nc - base) : kWave);
-        for (int jj = 0; jj < cnt; ++jj) {
-          const float wj = __shfl(wgt, jj, kWave);
-          const float* po = p.part_o + slot_of(v0 + base + jj) * HD;
+        for (int t = 0; t <= kSpec; ++t) {
+          int64_t u = t < 2 ? e : e + t - 1;
+          u = u < last_w ? u : last_w;
+          const int64_t sl = (u * 2 + (t == 1 ? 1 : 0)) * p.hg_max + h;
+          pm[j][t] = p.part_ml[sl * 2];
+          pl[j][t] = p.part_ml[sl * 2 + 1];
 #pragma unroll
           for (int q = 0; q < kPer; ++q) {
             const int d = lane + q * kWave;
-            if (d < HD) acc[q] += wj * po[d];
+            po[j][t][q] = d < HD ? p.part_o[sl * HD + d] : 0.f;
           }
         }
       }
+    }
+  };
+
+  int64_t e = blockIdx.x;  // < list_cap: the grid is at most list_cap workgroups
+  const int64_t total = p.hdr[0];
+  fetch(e);
+  if (total == 0) return;
+  const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
+  const int64_t n_slots = sc.nws + sc.nc < p.list_cap ? sc.nws + sc.nc : p.list_cap;
+  while (e < n_slots) {
+    const int64_t g0 = sg0;
+    if (g0 >= 0) {
+      const int64_t nb = snb;
+      const int64_t out_row = srow;
+      const int seg = static_cast<int>(sseg);
+      const int kvh = seg / p.head_chunks;
+      const int h0 = (seg % p.head_chunks) * 16;
+      const int hg = min(16, p.group - h0);
+      const int64_t v0 = vworker_of(sc, g0);
+      const int64_t v1 = vworker_of(sc, g0 + nb - 1);
+      const int64_t nc = v1 - v0 + 1;
+      auto slot_of = [&](int64_t u, int h) {
+        return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h;
+      };
+      if (v0 == e && nc <= kSpec) {
+        // the common case: everything is in registers already
+        const int t0 = vstart(sc, e) >= g0 ? 0 : 1;
 #pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) lsum += shfl_xor(lsum, off);
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        for (int j = 0; j < kHpw; ++j) {
+          const int h = wv + kWorkersPerGroup * j;
+          if (h >= hg) continue;
+          float big_m = -INFINITY;
 #pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        const int d = lane + q * kWave;
-        if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
+          for (int t = 1; t <= kSpec; ++t) {
+            const int k = t == 1 ? t0 : t;  // contributor t-1
+            if (t - 1 < nc) big_m = fmaxf(big_m, pm[j][k]);
+          }
+          const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
+          float lsum = 0.f;
+          float acc[kPer];
+#pragma unroll
+          for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
+#pragma unroll
+          for (int t = 1; t <= kSpec; ++t) {
+            const int k = t == 1 ? t0 : t;
+            if (t - 1 < nc) {
+              const float w = __builtin_amdgcn_exp2f(pm[j][k] - base_m);
+              lsum += w * pl[j][k];
+#pragma unroll
+              for (int q = 0; q < kPer; ++q) acc[q] += w * po[j][k][q];
+            }
+          }
+          const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+          const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
+#pragma unroll
+          for (int q = 0; q < kPer; ++q) {
+            const int d = lane + q * kWave;
+            if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
+          }
+        }
+      } else {
+        for (int h = wv; h < hg; h += kWorkersPerGroup) {
+          const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
+          float big_m = -INFINITY;
+          for (int64_t base = 0; base < nc; base += kWave) {
+            const int64_t j = base + lane;
+            const float m = j < nc ? p.part_ml[slot_of(v0 + j, h) * 2] : -INFINITY;
+            big_m = fmaxf(big_m, m);
+          }
+#pragma unroll
+          for (int off = 1; off < kWave; off <<= 1) big_m = fmaxf(big_m, shfl_xor(big_m, off));
+          const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
+
+          float lsum = 0.f;
+          float acc[kPer];
+#pragma unroll
+          for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
+          for (int64_t base = 0; base < nc; base += kWave) {
+            const int64_t j = base + lane;
+            float wgt = 0.f;
+            if (j < nc) {
+              const int64_t sl = slot_of(v0 + j, h);
+              wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
+              lsum += wgt * p.part_ml[sl * 2 + 1];
+            }
+            const int cnt = static_cast<int>((nc - base) < kWave ? (nc - base) : kWave);
+            for (int jj = 0; jj < cnt; ++jj) {
+              const float wj = __shfl(wgt, jj, kWave);
+              const float* o = p.part_o + slot_of(v0 + base + jj, h) * HD;
+#pragma unroll
+              for (int q = 0; q < kPer; ++q) {
+                const int d = lane + q * kWave;
+                if (d < HD) acc[q] += wj * o[d];
+              }
+            }
+          }
+#pragma unroll
+          for (int off = 1; off < kWave; off <<= 1) lsum += shfl_xor(lsum, off);
+          const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+          for (int q = 0; q < kPer; ++q) {
+            const int d = lane + q * kWave;
+            if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
+          }
+        }
       }
     }
+    e += gridDim.x;
+    if (e >= n_slots) break;
+    fetch(e);
   }
 }
 
