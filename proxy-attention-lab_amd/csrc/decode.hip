@@ -209,28 +209,37 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   }
 }
 
+// Item table of the in-LDS plan: length and page-table row of every item,
+// so a wavefront finds its next piece without a global round trip.
+struct ItemLds {
+  const int64_t* len;  // null: read items from global memory (item_at)
+  const int32_t* seq;
+};
+
 // Streams the blocks of virtual worker v (one wavefront), with the loads of
-// PF blocks in flight ahead of the one being computed.
+// PF blocks in flight ahead of the one being computed.  The range is a run
+// of pieces (the blocks of one segment inside the range); the pipeline runs
+// through piece boundaries: while the last blocks of a piece are computed,
+// the first blocks of the next piece are already loading (its item, query
+// and first page ids were fetched when the piece before it started).
 template <int DT, int HD, int TPP, int PF>
 __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched& sc, const int64_t* cum,
-                                              int64_t n_items, int64_t v) {
+                                              const ItemLds il, int64_t n_items, int64_t v) {
   constexpr bool kK32 = (HD % 32) == 0;  // QK k-step of 32 (else 16)
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
   constexpr int NT = HD / 16;            // output tiles of 16 dims
   constexpr int NBUF = PF + 1;
 
   const int64_t b0 = vstart(sc, v);
-  int64_t remaining = vstart(sc, v + 1) - b0;
+  const int64_t range_end = vstart(sc, v + 1);
   // merge-list slot of this virtual worker: written exactly once per call
   // (the split segment whose first piece ends this range, or 0), so the slot
   // never depends on what an earlier call left in the workspace
   int64_t list_g0 = -1, list_nb = 0, list_row = 0, list_seg = 0;  // g0 < 0: nothing to merge
-  if (remaining <= 0) {
+  if (range_end - b0 <= 0) {
     if (lane_id() == 0 && v < p.list_cap) p.split_list[4 * v] = -1;
     return;
   }
-  int64_t s = locate_seq(cum, n_items, b0);
-  int64_t r = b0 - cum[s];
 
   const int lane = lane_id();
   const int g = lane >> 4;
@@ -238,47 +247,159 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   const int segs = p.num_kv_heads * p.head_chunks;
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;  // elements per (page, kv head)
   const int64_t page_stride = head_block * p.num_kv_heads;
-  bool first = true;
-  int64_t gpos = b0;  // global block at which the current piece starts
 
-  while (remaining > 0) {
-    const Item it = item_at(p, s, TPP);
-    const int64_t len = it.len;
-    const int64_t nb = (len + 15) >> 4;
-    if (nb == 0) {  // empty sequence: no blocks, move on
-      ++s;
-      r = 0;
-      continue;
-    }
-    const int seg = static_cast<int>(r / nb);
-    const int64_t blk = r - seg * nb;
-    const int64_t count = (nb - blk) < remaining ? (nb - blk) : remaining;
-    const int kvh = seg / p.head_chunks;
+  // A piece: item s (query row s of page-table row `seq`, `len` keys, nb
+  // blocks per segment), segment `seg`, blocks [blk, blk + count) of the
+  // segment, starting at global block gpos; r = block offset of the piece
+  // inside the item's segments.  c_* is the piece being computed, x_* the
+  // next one (kept in scalars: the pipeline state must stay in registers).
+  int64_t c_s, c_r, c_gpos, c_seq, c_len, c_nb, c_blk, c_count;
+  int c_seg;
+  int64_t x_s, x_r, x_gpos, x_seq, x_len, x_nb, x_blk, x_count;
+  int x_seg;
+  // the piece at item s, offset r, global block gpos (items with no key
+  // have no blocks and are skipped)
+#define PAL_FIND_PIECE(P, S0, R0, G0)                                                              \
+  do {                                                                                             \
+    int64_t s_ = (S0), r_ = (R0), len_, seq_;                                                      \
+    for (;;) {                                                                                     \
+      if (il.len) {                                                                                \
+        len_ = il.len[s_];                                                                         \
+        seq_ = il.seq[s_];                                                                         \
+      } else {                                                                                     \
+        const Item it_ = item_at(p, s_, TPP);                                                      \
+        len_ = it_.len;                                                                            \
+        seq_ = it_.seq;                                                                            \
+      }                                                                                            \
+      if (len_ > 0) break;                                                                         \
+      ++s_;                                                                                        \
+      r_ = 0;                                                                                      \
+    }                                                                                              \
+    P##s = s_;                                                                                     \
+    P##r = r_;                                                                                     \
+    P##gpos = (G0);                                                                                \
+    P##seq = seq_;                                                                                 \
+    P##len = len_;                                                                                 \
+    P##nb = (len_ + 15) >> 4;                                                                      \
+    P##seg = static_cast<int>(r_ / P##nb);                                                         \
+    P##blk = r_ - P##seg * P##nb;                                                                  \
+    P##count = (P##nb - P##blk) < (range_end - P##gpos) ? (P##nb - P##blk) : (range_end - P##gpos); \
+  } while (0)
+
+  // Q^T operand of a piece: lane holds Q[head r16][k-slice of this lane]
+  // (padding heads zeroed).
+  u32x4 qv4[kK32 ? KK : 1], qn4[kK32 ? KK : 1];
+  u32x2 qv2[kK32 ? 1 : KK], qn2[kK32 ? 1 : KK];
+  auto load_q = [&](int64_t s, int seg, u32x4 (&q4)[kK32 ? KK : 1], u32x2 (&q2)[kK32 ? 1 : KK]) {
     const int h0 = (seg % p.head_chunks) * 16;
     const int hg = min(16, p.group - h0);
-    const int qh_base = kvh * p.group + h0;
-    const bool complete = (blk == 0) && (count == nb);
+    const int qh_base = (seg / p.head_chunks) * p.group + h0;
+    const bool hv = r16 < hg;
+    const uint32_t qmask = hv ? 0xFFFFFFFFu : 0u;
+    const uint16_t* qrow = p.q + (s * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if constexpr (kK32) {
+        q4[kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * g) & qmask;
+      } else {
+        q2[kk] = *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 4 * g) & qmask;
+      }
+    }
+  };
+  // page ids of window wi (64 pages, one per lane) of a piece
+  auto load_window = [&](int64_t seq, int64_t blk, int64_t wi) {
+    const uint32_t* pt = p.page_table + seq * p.page_table_width;
+    int64_t lp = (blk * 16) / TPP + wi * kWave + lane;
+    if (lp >= p.page_table_width) lp = p.page_table_width - 1;
+    return pt[lp];
+  };
 
-    // Q^T operand: lane holds Q[head r16][k-slice of this lane] (padding heads zeroed).
-    u32x4 qv4[kK32 ? KK : 1];
-    u32x2 qv2[kK32 ? 1 : KK];
-    {
-      const bool hv = r16 < hg;
-      const uint32_t qmask = hv ? 0xFFFFFFFFu : 0u;
-      const uint16_t* qrow = p.q + (it.row * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
+  {
+    const int64_t s0 = locate_seq(cum, n_items, b0);  // the item holding block b0 (it has blocks)
+    PAL_FIND_PIECE(c_, s0, b0 - cum[s0], b0);
+  }
+  load_q(c_s, c_seg, qv4, qv2);
+
+  // Page ids in register windows of 64 pages (one id per lane): pid_cur
+  // holds window wcur, the window of the block being computed, and pid_nxt
+  // window wcur+1 (the loads run at most a few blocks ahead).  Every step
+  // group also loads window wcur+2 (unconditionally, so the vector-memory
+  // stream of the loop is the same every time and the compiler's counted
+  // waits stay exact); when the computed block enters window wcur+1 the
+  // windows move up by one, taking the window wcur+2 loaded a step group
+  // earlier.
+  int64_t wcur = 0;
+  uint32_t pid_cur = load_window(c_seq, c_blk, 0), pid_nxt = load_window(c_seq, c_blk, 1),
+           pid_later = load_window(c_seq, c_blk, 2);
+
+  u32x4 kb4[NBUF][kK32 ? KK : 1];
+  u32x2 kb2[NBUF][kK32 ? 1 : KK];
+  u32x2 vb[NBUF][NT];
+  bool bv[NBUF];
+
+  bool first = true;
+  bool has_next = false;
+  x_s = c_s; x_r = c_r; x_gpos = c_gpos; x_seq = c_seq; x_len = c_len; x_nb = c_nb; x_blk = c_blk;
+  x_count = c_count; x_seg = c_seg;
+  uint32_t pidn0 = 0;  // window 0 of the next piece
+
+  for (;;) {
+    const int kvh = c_seg / p.head_chunks;
+    const int h0 = (c_seg % p.head_chunks) * 16;
+    const int hg = min(16, p.group - h0);
+    const int qh_base = kvh * p.group + h0;
+    const bool complete = (c_blk == 0) && (c_count == c_nb);
+    const int64_t len = c_len;
+    const int64_t n_blk = c_count;
+    const int64_t n_pad = (n_blk + NBUF - 1) / NBUF * NBUF;  // steps of the piece
+    const int64_t bstart = c_blk;                          // first block of the piece
+    const int64_t pbase = (bstart * 16) / TPP;               // its page index
+    const uint16_t* kbase = p.k_pool + kvh * head_block;
+    const uint16_t* vbase = p.v_pool + kvh * head_block;
+    const uint16_t* kbase_n = kbase;  // set once the next piece is known
+    const uint16_t* vbase_n = vbase;
+    int64_t nblk_n = 1;
+
+    // Issue the K and V loads of step i of the piece into buffer `buf`:
+    // block i of the piece (clamped to its last block), or, past the
+    // piece's steps, block i - n_pad of the next piece (which starts at
+    // block 0 of its segment).  An out-of-range page id is replaced by page
+    // 0 (in bounds) and the block is masked out when computed.  Every K/V
+    // block is read exactly once per call, so the loads carry the
+    // non-temporal hint: the stream does not displace other lines (page ids,
+    // partials, the fused op's prefill tiles) from L2 and MALL.
+    auto issue = [&](int64_t i, int buf) {
+      const bool to_next = has_next && i >= n_pad;
+      const int64_t j = to_next ? (i - n_pad < nblk_n - 1 ? i - n_pad : nblk_n - 1) : (i < n_blk - 1 ? i : n_blk - 1);
+      const int64_t b = (to_next ? 0 : bstart) + j;
+      const int64_t e = (b * 16) / TPP - (to_next ? 0 : pbase);  // page of the piece
+      // (selects of values, not of variables: a select of two variables'
+      // addresses would push the whole pipeline state to scratch)
+      const uint32_t w_n0 = pidn0, w_c = pid_cur, w_x = pid_nxt;
+      const uint32_t win = to_next ? w_n0 : ((e >> 6) == wcur ? w_c : w_x);
+      const uint32_t pg = __builtin_amdgcn_readlane(win, static_cast<int>(e & 63));
+      bv[buf] = pg < p.num_pages;
+      const uint32_t page = bv[buf] ? pg : 0u;
+      const int slot0 = static_cast<int>((b * 16) % TPP);
+      const uint16_t* kb_x = kbase_n;
+      const uint16_t* vb_x = vbase_n;
+      const uint16_t* kp = (to_next ? kb_x : kbase) + static_cast<int64_t>(page) * page_stride;
+      const uint16_t* vp = (to_next ? vb_x : vbase) + static_cast<int64_t>(page) * page_stride + slot0 + 4 * g;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         if constexpr (kK32) {
-          qv4[kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * g) & qmask;
+          const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
+          kb4[buf][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8));
         } else {
-          qv2[kk] = *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 4 * g) & qmask;
+          const int d = 16 * kk + 4 * g;  // dims d .. d+3
+          kb2[buf][kk] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x2*>(kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7)));
         }
       }
-    }
-
-    const uint16_t* kbase = p.k_pool + kvh * head_block;
-    const uint16_t* vbase = p.v_pool + kvh * head_block;
-    const uint32_t* pt = p.page_table + it.seq * p.page_table_width;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        vb[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP));
+    };
 
     float m_run = -INFINITY;  // running max (raw score units) of head r16
     float l_run = 0.f;        // this lane's share of the exp-sum of head r16
@@ -286,145 +407,133 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    {
-      // Page ids in register windows of 64 pages (one id per lane): pid_cur
-      // holds window wcur, the window of the block being computed, and
-      // pid_nxt window wcur+1 (the loads run at most a few blocks ahead).
-      // Every step group also loads window wcur+2 (unconditionally, so the
-      // vector-memory stream of the loop is the same every time and the
-      // compiler's counted waits stay exact); when the computed block
-      // enters window wcur+1 the windows move up by one, taking the window
-      // wcur+2 loaded a step group earlier.  The K/V pipeline never stops for
-      // page ids inside a piece.
-      const int64_t n_blk = count;
-      const int64_t bstart = blk;                 // first block of the piece
-      const int64_t pbase = (bstart * 16) / TPP;  // its page index
-      auto load_window = [&](int64_t wi) {
-        int64_t lp = pbase + wi * kWave + lane;
-        if (lp >= p.page_table_width) lp = p.page_table_width - 1;
-        return pt[lp];
-      };
-      int64_t wcur = 0;
-      uint32_t pid_cur = load_window(0), pid_nxt = load_window(1), pid_later = load_window(2);
-
-      u32x4 kb4[NBUF][kK32 ? KK : 1];
-      u32x2 kb2[NBUF][kK32 ? 1 : KK];
-      u32x2 vb[NBUF][NT];
-      bool bv[NBUF];
-
-      // Issue the K and V loads of block i of the piece into buffer `buf`.
-      // An out-of-range page id is replaced by page 0 (in bounds) and the
-      // block is masked out when computed.  Every K/V block is read exactly
-      // once per call, so the loads carry the non-temporal hint: the stream
-      // does not displace other lines (page ids, partials, the fused op's
-      // prefill tiles) from L2 and MALL.
-      auto issue = [&](int64_t i, int buf) {
-        const int64_t b = bstart + i;
-        const int64_t e = (b * 16) / TPP - pbase;  // page of the piece
-        const uint32_t pg = __builtin_amdgcn_readlane((e >> 6) == wcur ? pid_cur : pid_nxt, static_cast<int>(e & 63));
-        bv[buf] = pg < p.num_pages;
-        const uint32_t page = bv[buf] ? pg : 0u;
-        const int slot0 = static_cast<int>((b * 16) % TPP);
-        const uint16_t* kp = kbase + static_cast<int64_t>(page) * page_stride;
-        const uint16_t* vp = vbase + static_cast<int64_t>(page) * page_stride + slot0 + 4 * g;
+    auto compute = [&](int64_t i, int buf) {
+      const int64_t b = bstart + i;
+      const bool live = bv[buf] && i < n_blk;  // steps past the piece end are fully masked
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          if constexpr (kK32) {
-            const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
-            kb4[buf][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8));
-          } else {
-            const int d = 16 * kk + 4 * g;  // dims d .. d+3
-            kb2[buf][kk] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x2*>(kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7)));
-          }
+      for (int kk = 0; kk < KK; ++kk) {
+        if constexpr (kK32) {
+          acc = Dt<DT>::mma16x16x32(kb4[buf][kk], qv4[kk], acc);
+        } else {
+          acc = Dt<DT>::mma16x16x16(kb2[buf][kk], qv2[kk], acc);
         }
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-          vb[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP));
-      };
-
-      auto compute = [&](int64_t i, int buf) {
-        const int64_t b = bstart + i;
-        const bool live = bv[buf] && i < n_blk;  // steps past the chunk end are fully masked
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          if constexpr (kK32) {
-            acc = Dt<DT>::mma16x16x32(kb4[buf][kk], qv4[kk], acc);
-          } else {
-            acc = Dt<DT>::mma16x16x16(kb2[buf][kk], qv2[kk], acc);
-          }
-        }
-        // tokens past the end (and whole invalid blocks) are masked
-        const int64_t t0 = live ? b * 16 + 4 * g : len;
-        float sc4[4];
-        float bm = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sc4[e] = (t0 + e < len) ? acc[e] : -INFINITY;
-          bm = fmaxf(bm, sc4[e]);
-        }
-        bm = fmaxf(bm, shfl_xor(bm, 16));
-        bm = fmaxf(bm, shfl_xor(bm, 32));
-        const float m_new = fmaxf(m_run, bm);
-        const float msc = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
-        if (__ballot(m_new > m_run && m_run != -INFINITY)) {
-          // the max of some head grew: rescale the running state
-          const float alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(fmaf(m_run, p.scale_log2, -msc));
-          l_run *= alpha;
-#pragma unroll
-          for (int n = 0; n < NT; ++n) o[n] *= alpha;
-        }
-        m_run = m_new;
-        float pe[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pe[e] = __builtin_amdgcn_exp2f(fmaf(sc4[e], p.scale_log2, -msc));
-          l_run += pe[e];
-        }
-        const u32x2 pb = {Dt<DT>::pack2(pe[0], pe[1]), Dt<DT>::pack2(pe[2], pe[3])};
-        // slots past the end may hold anything, NaN bits included: zero their
-        // V (branch-free: two ANDs per tile)
-        const uint32_t mlo = (t0 < len ? 0x0000FFFFu : 0u) | (t0 + 1 < len ? 0xFFFF0000u : 0u);
-        const uint32_t mhi = (t0 + 2 < len ? 0x0000FFFFu : 0u) | (t0 + 3 < len ? 0xFFFF0000u : 0u);
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          const u32x2 vv = {vb[buf][n].x & mlo, vb[buf][n].y & mhi};
-          o[n] = Dt<DT>::mma16x16x16(vv, pb, o[n]);
-        }
-      };
-
-      // Every step issues and computes unconditionally (steps past the end
-      // re-read the last block, an L2 hit, and compute it fully masked): with
-      // no load under a branch the compiler's wait counts stay exact, so the
-      // PF blocks in flight are never drained early.
-#pragma unroll
-      for (int q = 0; q < PF; ++q) issue(q < n_blk ? q : n_blk - 1, q);
-      for (int64_t i0 = 0; i0 < n_blk; i0 += NBUF) {
-        const uint32_t pid_ahead = load_window(wcur + 2);
-#pragma unroll
-        for (int u = 0; u < NBUF; ++u) {
-          const int64_t i = i0 + u;
-          issue(i + PF < n_blk ? i + PF : n_blk - 1, (u + PF) % NBUF);
-          compute(i, u);
-        }
-        // entered window wcur+1: move the windows up (at most NBUF + PF pages
-        // past its start, so no issue has needed window wcur+2 yet)
-        const int64_t e_last = ((bstart + i0 + NBUF - 1) * 16) / TPP - pbase;
-        const bool up = (e_last >> 6) > wcur;
-        pid_cur = up ? pid_nxt : pid_cur;
-        pid_nxt = up ? pid_later : pid_nxt;
-        wcur += up ? 1 : 0;
-        pid_later = pid_ahead;
       }
+      // tokens past the end (and whole invalid blocks) are masked
+      const int64_t t0 = live ? b * 16 + 4 * g : len;
+      float sc4[4];
+      float bm = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sc4[e] = (t0 + e < len) ? acc[e] : -INFINITY;
+        bm = fmaxf(bm, sc4[e]);
+      }
+      bm = fmaxf(bm, shfl_xor(bm, 16));
+      bm = fmaxf(bm, shfl_xor(bm, 32));
+      const float m_new = fmaxf(m_run, bm);
+      const float msc = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
+      if (__ballot(m_new > m_run && m_run != -INFINITY)) {
+        // the max of some head grew: rescale the running state
+        const float alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(fmaf(m_run, p.scale_log2, -msc));
+        l_run *= alpha;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) o[n] *= alpha;
+      }
+      m_run = m_new;
+      float pe[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pe[e] = __builtin_amdgcn_exp2f(fmaf(sc4[e], p.scale_log2, -msc));
+        l_run += pe[e];
+      }
+      const u32x2 pb = {Dt<DT>::pack2(pe[0], pe[1]), Dt<DT>::pack2(pe[2], pe[3])};
+      // slots past the end may hold anything, NaN bits included: zero their
+      // V (branch-free: two ANDs per tile)
+      const uint32_t mlo = (t0 < len ? 0x0000FFFFu : 0u) | (t0 + 1 < len ? 0xFFFF0000u : 0u);
+      const uint32_t mhi = (t0 + 2 < len ? 0x0000FFFFu : 0u) | (t0 + 3 < len ? 0xFFFF0000u : 0u);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const u32x2 vv = {vb[buf][n].x & mlo, vb[buf][n].y & mhi};
+        o[n] = Dt<DT>::mma16x16x16(vv, pb, o[n]);
+      }
+    };
+
+    // The first piece fills the pipeline; a later piece finds its first PF
+    // blocks in flight already.
+    if (first) {
+#pragma unroll
+      for (int q = 0; q < PF; ++q) issue(q, q);
     }
+
+    // The next piece: its item, query and first page ids load now, while
+    // this piece streams.  (With no next piece the current one is loaded
+    // again, so these loads are unconditional.)
+    {
+      const int64_t gpos_n = c_gpos + c_count;
+      has_next = gpos_n < range_end;
+      int64_t s_n = c_s, r_n = c_r + c_count;
+      if (r_n >= c_nb * segs) {
+        ++s_n;
+        r_n = 0;
+      }
+      if (has_next) {
+        PAL_FIND_PIECE(x_, s_n, r_n, gpos_n);
+      } else {
+        x_s = c_s; x_r = c_r; x_gpos = c_gpos; x_seq = c_seq; x_len = c_len; x_nb = c_nb; x_blk = c_blk;
+        x_count = c_count; x_seg = c_seg;
+      }
+      load_q(x_s, x_seg, qn4, qn2);
+      pidn0 = load_window(x_seq, x_blk, 0);
+    }
+    const uint32_t pidn1 = load_window(x_seq, x_blk, 1);
+    {
+      const int kvh_x = x_seg / p.head_chunks;
+      kbase_n = p.k_pool + kvh_x * head_block;
+      vbase_n = p.v_pool + kvh_x * head_block;
+      nblk_n = x_count;
+    }
+
+    // Every step issues and computes unconditionally (steps past the end
+    // re-read the last block, an L2 hit, and compute it fully masked): with
+    // no load under a branch the compiler's wait counts stay exact, so the
+    // PF blocks in flight are never drained early.
+    // (n_pad >= NBUF: at least one step group, which the do-while tells the
+    // compiler, so no path reaches the hand-over without the waits below)
+    int64_t i0 = 0;
+    do {
+      const uint32_t pid_ahead = load_window(c_seq, c_blk, wcur + 2);
+#pragma unroll
+      for (int u = 0; u < NBUF; ++u) {
+        const int64_t i = i0 + u;
+        issue(i + PF, (u + PF) % NBUF);
+        compute(i, u);
+      }
+      // entered window wcur+1: move the windows up (at most NBUF + PF pages
+      // past its start, so no issue has needed window wcur+2 yet)
+      const int64_t e_last = ((bstart + i0 + NBUF - 1) * 16) / TPP - pbase;
+      const bool up = (e_last >> 6) > wcur;
+      pid_cur = up ? pid_nxt : pid_cur;
+      pid_nxt = up ? pid_later : pid_nxt;
+      wcur += up ? 1 : 0;
+      pid_later = pid_ahead;
+      // The next piece's query and page ids must have arrived by the end of
+      // the first step group (they are older than its loads): consume them
+      // here, where the wait count is exact, so the piece hand-over below
+      // does not wait on the loads in flight.
+#pragma unroll
+      for (int kk = 0; kk < (kK32 ? KK : 1); ++kk) asm volatile("" ::"v"(qn4[kk]));
+#pragma unroll
+      for (int kk = 0; kk < (kK32 ? 1 : KK); ++kk) asm volatile("" ::"v"(qn2[kk]));
+      asm volatile("" ::"v"(pidn0), "v"(pidn1));
+      i0 += NBUF;
+    } while (i0 < n_pad);
 
     // ---- finish the segment piece: exp-sum of head r16 over the 4 lane groups
     float l = l_run;
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
     if (r16 < hg) {
-      const int64_t row = it.row * p.num_q_heads + qh_base + r16;
+      const int64_t row = c_s * p.num_q_heads + qh_base + r16;
       if (complete) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
@@ -437,29 +546,35 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #pragma unroll
         for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(p.part_o + slot * HD + 16 * n + 4 * g) = o[n];
         if (g == 0) {
-          p.part_ml[slot * 2 + 0] = (m_run == -INFINITY) ? -INFINITY : m_run * p.scale_log2;
-          p.part_ml[slot * 2 + 1] = l;
+          const f32x2 ml = {(m_run == -INFINITY) ? -INFINITY : m_run * p.scale_log2, l};
+          *reinterpret_cast<f32x2*>(p.part_ml + slot * 2) = ml;
         }
       }
     }
 
     // the first piece of a split segment can only end the range (a range
     // ends inside one segment): that segment goes on the merge list
-    if (!complete && blk == 0) {
-      list_g0 = gpos;  // the piece starts the segment
-      list_nb = nb;
-      list_row = it.row;
-      list_seg = seg;
-    }
-
-    remaining -= count;
-    gpos += count;
-    r += count;
-    if (r >= nb * segs) {
-      ++s;
-      r = 0;
+    if (!complete && c_blk == 0) {
+      list_g0 = c_gpos;  // the piece starts the segment
+      list_nb = c_nb;
+      list_row = c_s;
+      list_seg = c_seg;
     }
     first = false;
+    if (!has_next) break;
+
+    // the next piece becomes current: its first PF blocks are in flight,
+    // in buffers 0 .. PF-1 (n_pad is a multiple of NBUF)
+    c_s = x_s; c_r = x_r; c_gpos = x_gpos; c_seq = x_seq; c_len = x_len; c_nb = x_nb; c_blk = x_blk;
+    c_count = x_count; c_seg = x_seg;
+#pragma unroll
+    for (int kk = 0; kk < (kK32 ? KK : 1); ++kk) qv4[kk] = qn4[kk];
+#pragma unroll
+    for (int kk = 0; kk < (kK32 ? 1 : KK); ++kk) qv2[kk] = qn2[kk];
+    wcur = 0;
+    pid_cur = pidn0;
+    pid_nxt = pidn1;
+    pid_later = load_window(c_seq, c_blk, 2);
   }
   if (lane_id() == 0 && v < p.list_cap) {
     int64_t* slot = p.split_list + 4 * v;
@@ -468,10 +583,12 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     slot[2] = list_row;
     slot[3] = list_seg;
   }
+#undef PAL_FIND_PIECE
 }
 
 template <int DT, int HD, int TPP, int PF>
-__device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_lds, int64_t* wave_sums) {
+__device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_lds, int64_t* len_lds,
+                                            int32_t* seq_lds, int64_t* wave_sums) {
   const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
   const int64_t* cum = p.cum;
   int64_t total = 0;
@@ -491,6 +608,8 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
       if (s < n_items) {
         const Item it = item_at(p, s, TPP);
         vals[k] = ((it.len + 15) >> 4) * segs;
+        len_lds[s] = it.len;
+        seq_lds[s] = static_cast<int32_t>(it.seq);
         // empty items get zeros, written once, by workgroup 0
         if (it.len == 0 && !it.skip && blockIdx.x == 0) zero_item_output<HD>(p, it.row);
       }
@@ -516,15 +635,16 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
     total = p.hdr[0];
   }
   if (total == 0) return;
+  const ItemLds il = lds_plan ? ItemLds{len_lds, seq_lds} : ItemLds{nullptr, nullptr};
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
   const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (w < sc.nws) process_range<DT, HD, TPP, PF>(p, sc, cum, n_items, w);
+  if (w < sc.nws) process_range<DT, HD, TPP, PF>(p, sc, cum, il, n_items, w);
   while (sc.nc > 0) {
     uint32_t k = 0;
     if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
     k = __builtin_amdgcn_readfirstlane(k);
     if (k >= sc.nc) break;
-    process_range<DT, HD, TPP, PF>(p, sc, cum, n_items, sc.nws + k);
+    process_range<DT, HD, TPP, PF>(p, sc, cum, il, n_items, sc.nws + k);
   }
 }
 
@@ -534,8 +654,10 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const DecodeParams p) {
   __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
+  __shared__ int64_t len_lds[kInlinePlanSeqs];
+  __shared__ int32_t seq_lds[kInlinePlanSeqs];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, kPrefetch>(p, cum_lds, wave_sums);
+  stream_body<DT, HD, TPP, kPrefetch>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Decode rows of the fused op: one workgroup per CU, held to half of the
@@ -549,15 +671,17 @@ constexpr bool shares_cu(int hd) { return hd <= 128; }
 
 template <int HD, int TPP>
 constexpr int shared_cu_prefetch() {
-  return HD == 128 && TPP == 32 ? kPrefetch - 1 : kPrefetch;
+  return HD == 128 ? kPrefetch - 1 : kPrefetch;
 }
 
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_shared_cu_kernel(const DecodeParams p) {
   __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
+  __shared__ int64_t len_lds[kInlinePlanSeqs];
+  __shared__ int32_t seq_lds[kInlinePlanSeqs];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>()>(p, cum_lds, wave_sums);
+  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>()>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Walks the merge list, slot v for virtual worker v (first block < 0:
