@@ -88,9 +88,9 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
  * Workspace bytes pal_paged_attention_decode needs for these shapes on the
  * current device (0 for unsupported arguments or when no device is present).
  * The workspace holds a scan of the sequence lengths, a work-claim counter
- * and the fp32 partials (max, exp-sum, unnormalised output) of KV segments
- * split between workers; its size follows from the number of wavefront
- * workers the device keeps resident.
+ * and the partials (fp32 max and exp-sum, output / exp-sum in the query
+ * dtype) of KV segments split between workers; its size follows from the
+ * number of wavefront workers the device keeps resident.
  * partition_size: 0 (default: the KV blocks of the batch are cut into one
  * equal share per resident worker) or 128 / 256 / 512: fixed chunks of that
  * many tokens, claimed by whichever worker is free and merged by log-sum-exp
@@ -114,7 +114,7 @@ size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, in
  * The KV blocks of all sequences are split evenly over the device's
  * resident workers; a sequence split between workers is merged with a
  * log-sum-exp pass (the reference's two-pass mode,
- * decode_primitive.cpp:100-102,163-240) from fp32 partials.  The workspace
+ * decode_primitive.cpp:100-102,163-240) from the partials.  The workspace
  * (256-byte aligned, size from pal_paged_attention_decode_workspace_size,
  * zero-filled before its first use) must not be shared by calls that can
  * run concurrently.

@@ -39,11 +39,11 @@
 //    the prefill kernel and are skipped here.  Plain decode: item i is query
 //    row i of sequence i.
 //  * A segment that lies wholly inside one virtual worker writes the
-//    normalised output directly.  Split segments leave fp32 partials
-//    (max, exp-sum, unnormalised O) in one of two slots per virtual worker,
-//    combined by decode_merge_kernel.  The worker holding the first piece of
-//    a split segment writes it into its own slot of a merge list, so the
-//    merge grid does not grow with the batch.
+//    normalised output directly.  Split segments leave partials (fp32 max
+//    and exp-sum, O / exp-sum in the 16-bit dtype) in one of two slots per
+//    virtual worker, combined by decode_merge_kernel.  The worker holding the
+//    first piece of a split segment writes it into its own slot of a merge
+//    list, so the merge grid does not grow with the batch.
 #include "pal_device.h"
 
 namespace pal {
@@ -542,9 +542,16 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
           *reinterpret_cast<u32x2*>(p.out + row * HD + 16 * n + 4 * g) = pk;
         }
       } else {
+        // partial: (max, exp-sum) in fp32 and O / exp-sum in the 16-bit
+        // dtype (half the bytes of fp32 O; the rounding is that of one more
+        // output store)
         const int64_t slot = (v * 2 + (first ? 0 : 1)) * p.hg_max + r16;
+        const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(p.part_o + slot * HD + 16 * n + 4 * g) = o[n];
+        for (int n = 0; n < NT; ++n) {
+          const u32x2 pk = {Dt<DT>::pack2(o[n][0] * inv, o[n][1] * inv), Dt<DT>::pack2(o[n][2] * inv, o[n][3] * inv)};
+          *reinterpret_cast<u32x2*>(p.part_o + slot * HD + 16 * n + 4 * g) = pk;
+        }
         if (g == 0) {
           const f32x2 ml = {(m_run == -INFINITY) ? -INFINITY : m_run * p.scale_log2, l};
           *reinterpret_cast<f32x2*>(p.part_ml + slot * 2) = ml;
@@ -690,8 +697,9 @@ void decode_shared_cu_kernel(const DecodeParams p) {
 // segment index, so the merge needs no other lookup); a workgroup per slot
 // at a time, the grid striding over the live workers.  A split segment
 // (sequence, kv head, head chunk) is merged head by head, a wavefront per
-// head: M = max_c m_c, out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c
-// over the virtual workers c that shared it.
+// head: M = max_c m_c, w_c = 2^(m_c - M) l_c, out = sum_c w_c Y_c / sum_c w_c
+// over the virtual workers c that shared it (Y_c = O_c / l_c, the stored
+// normalised partial).
 //
 // The worker that wrote slot v holds the segment's first piece, so the
 // contributors are v, v+1, ...: the list slot, the header and the partials of
@@ -734,7 +742,7 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
 #pragma unroll
           for (int q = 0; q < kPer; ++q) {
             const int d = lane + q * kWave;
-            po[j][t][q] = d < HD ? p.part_o[sl * HD + d] : 0.f;
+            po[j][t][q] = d < HD ? Dt<DT>::to_f32(p.part_o[sl * HD + d]) : 0.f;
           }
         }
       }
@@ -784,8 +792,8 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
           for (int t = 1; t <= kSpec; ++t) {
             const int k = t == 1 ? t0 : t;
             if (t - 1 < nc) {
-              const float w = __builtin_amdgcn_exp2f(pm[j][k] - base_m);
-              lsum += w * pl[j][k];
+              const float w = __builtin_amdgcn_exp2f(pm[j][k] - base_m) * pl[j][k];
+              lsum += w;
 #pragma unroll
               for (int q = 0; q < kPer; ++q) acc[q] += w * po[j][k][q];
             }
@@ -820,17 +828,17 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
             float wgt = 0.f;
             if (j < nc) {
               const int64_t sl = slot_of(v0 + j, h);
-              wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m);
-              lsum += wgt * p.part_ml[sl * 2 + 1];
+              wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m) * p.part_ml[sl * 2 + 1];
+              lsum += wgt;
             }
             const int cnt = static_cast<int>((nc - base) < kWave ? (nc - base) : kWave);
             for (int jj = 0; jj < cnt; ++jj) {
               const float wj = __shfl(wgt, jj, kWave);
-              const float* o = p.part_o + slot_of(v0 + base + jj, h) * HD;
+              const uint16_t* o = p.part_o + slot_of(v0 + base + jj, h) * HD;
 #pragma unroll
               for (int q = 0; q < kPer; ++q) {
                 const int d = lane + q * kWave;
-                if (d < HD) acc[q] += wj * o[d];
+                if (d < HD) acc[q] += wj * Dt<DT>::to_f32(o[d]);
               }
             }
           }

@@ -84,7 +84,7 @@ DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t v
   l.part_ml = off;
   off += align256(static_cast<size_t>(virtual_workers) * 2 * hg_max * 2 * sizeof(float));
   l.part_o = off;
-  off += align256(static_cast<size_t>(virtual_workers) * 2 * hg_max * head_dim * sizeof(float));
+  off += align256(static_cast<size_t>(virtual_workers) * 2 * hg_max * head_dim * sizeof(uint16_t));
   l.total = off;
   return l;
 }
@@ -164,7 +164,7 @@ pal::DecodeParams decode_params(const void* queries, const void* k_pool, const v
   p.list_cap = lay.list_cap;
   p.cum = reinterpret_cast<int64_t*>(ws + lay.cum);
   p.part_ml = reinterpret_cast<float*>(ws + lay.part_ml);
-  p.part_o = reinterpret_cast<float*>(ws + lay.part_o);
+  p.part_o = reinterpret_cast<uint16_t*>(ws + lay.part_o);
   p.num_seqs = num_items;
   p.num_pages = num_pages;
   p.page_table_width = page_table_width;

@@ -57,7 +57,7 @@ struct DecodeParams {
   int64_t list_cap;
   int64_t* cum;                // [S + 1] first global block of each sequence
   float* part_ml;              // [virtual workers][2][hg_max][2] (max * log2e * scale, exp-sum)
-  float* part_o;               // [virtual workers][2][hg_max][HD]  unnormalised O
+  uint16_t* part_o;            // [virtual workers][2][hg_max][HD]  O / exp-sum, 16-bit dtype
   int64_t num_seqs;       // items (row mode: query rows)
   int64_t num_pages;
   int64_t page_table_width;

@@ -161,3 +161,15 @@ def test_decode_many_short_sequences():
     case = make_paged_case(15, lens, 8, 2, 64, 16, "bf16", garbage_tail=False)
     q = randn_bits(rng, (1500, 8, 64), "bf16")
     _check(case, q, what="1500 sequences")
+
+
+def test_decode_many_pieces_per_worker():
+    """900 short sequences (the in-kernel planner's item table), zeros among
+    them: every wavefront streams many segment pieces back to back, so the
+    next piece's blocks load while the current piece finishes."""
+    rng = np.random.default_rng(16)
+    lens = rng.integers(0, 200, size=900).astype(np.int32)
+    lens[rng.choice(900, 60, replace=False)] = 0
+    case = make_paged_case(16, lens, 32, 8, 128, 16, "bf16", garbage_tail=True)
+    q = randn_bits(rng, (900, 32, 128), "bf16")
+    _check(case, q, what="900 sequences")
