@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
   const int lane = lane_id();
   const int wv = wave_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
-  constexpr int kSpec = 4;                              // contributors fetched with the slot
+  constexpr int kSpec = 3;                              // contributors fetched with the slot
   constexpr int kHpw = 16 / kWorkersPerGroup;           // heads per wavefront (hg_max <= 16)
   const int64_t last_w = p.list_cap - 1;                // partial slots exist for workers < list_cap
 
