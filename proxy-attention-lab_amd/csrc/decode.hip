@@ -881,7 +881,13 @@ hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t st
                        dim3(kGroupThreads), 0, stream, p);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
-  const int64_t merge_groups = p.list_cap < kMergeGroups ? p.list_cap : kMergeGroups;
+  // Live merge slots: one per static share (at most num_workers) with equal
+  // shares, up to list_cap in the fixed-chunk mode.  A workgroup with no
+  // live slot still pays one fetch round trip, so the equal-share grid is
+  // not padded beyond the workers (it then fits the GPU in one round).
+  const bool all_static = p.tokens_per_worker == 0 && kStaticShareNum == kStaticShareDen;
+  int64_t merge_groups = all_static ? p.num_workers : kMergeGroups;
+  if (merge_groups > p.list_cap) merge_groups = p.list_cap;
   hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(merge_groups)),
                      dim3(kGroupThreads), 0, stream, p);
   return hipGetLastError();
