@@ -716,6 +716,7 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
   const int wv = wave_id();
   constexpr int kPer = (HD + kWave - 1) / kWave;
   constexpr int kSpec = 3;                              // contributors fetched with the slot
+  constexpr int kBatch = 8;                             // general path: O loads in flight
   constexpr int kHpw = 16 / kWorkersPerGroup;           // heads per wavefront (hg_max <= 16)
   const int64_t last_w = p.list_cap - 1;                // partial slots exist for workers < list_cap
 
@@ -832,13 +833,26 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
               lsum += wgt;
             }
             const int cnt = static_cast<int>((nc - base) < kWave ? (nc - base) : kWave);
-            for (int jj = 0; jj < cnt; ++jj) {
-              const float wj = __shfl(wgt, jj, kWave);
-              const uint16_t* o = p.part_o + slot_of(v0 + base + jj, h) * HD;
+            // kBatch contributors' O loads in flight at a time (a load per
+            // contributor and a wait each would make the merge of a long
+            // sequence split into many chunks a chain of round trips)
+            for (int jj0 = 0; jj0 < cnt; jj0 += kBatch) {
+              uint16_t ob[kBatch][kPer];
 #pragma unroll
-              for (int q = 0; q < kPer; ++q) {
-                const int d = lane + q * kWave;
-                if (d < HD) acc[q] += wj * Dt<DT>::to_f32(o[d]);
+              for (int u = 0; u < kBatch; ++u) {
+                const int jj = jj0 + u < cnt ? jj0 + u : cnt - 1;  // padding re-reads the last one
+                const uint16_t* o = p.part_o + slot_of(v0 + base + jj, h) * HD;
+#pragma unroll
+                for (int q = 0; q < kPer; ++q) {
+                  const int d = lane + q * kWave;
+                  ob[u][q] = d < HD ? o[d] : uint16_t{0};
+                }
+              }
+#pragma unroll
+              for (int u = 0; u < kBatch; ++u) {
+                const float wj = jj0 + u < cnt ? __shfl(wgt, jj0 + u, kWave) : 0.f;
+#pragma unroll
+                for (int q = 0; q < kPer; ++q) acc[q] += wj * Dt<DT>::to_f32(ob[u][q]);
               }
             }
           }
