@@ -768,9 +768,6 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
       const int64_t v0 = vworker_of(sc, g0);
       const int64_t v1 = vworker_of(sc, g0 + nb - 1);
       const int64_t nc = v1 - v0 + 1;
-      auto slot_of = [&](int64_t u, int h) {
-        return (u * 2 + (vstart(sc, u) >= g0 ? 0 : 1)) * p.hg_max + h;
-      };
       if (v0 == e && nc <= kSpec) {
         // the common case: everything is in registers already
         const int t0 = vstart(sc, e) >= g0 ? 0 : 1;
@@ -808,61 +805,72 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
           }
         }
       } else {
+        // General path: a lane group of kLpr lanes holds one contributor's
+        // row (8 dims per lane, one 16-byte load), so one load instruction
+        // covers kRpi contributors and kBatch instructions are in flight;
+        // the row groups' sums are combined with shuffles at the end.
+        // Contributor 0 is worker v0's piece in partial slot t0; every later
+        // contributor's piece is its first (slot 0).
+        constexpr int kLpr = HD <= 32 ? 4 : (HD <= 64 ? 8 : (HD <= 128 ? 16 : 32));  // >= HD / 8
+        constexpr int kRpi = kWave / kLpr;
+        const int rl = lane % kLpr;  // 8-dim slice of the row
+        const int rg = lane / kLpr;  // row within one load instruction
+        const bool dl = rl * 8 < HD;
+        const int t0 = vstart(sc, v0) >= g0 ? 0 : 1;
+        auto slot_j = [&](int64_t j, int h) { return ((v0 + j) * 2 + (j == 0 ? t0 : 0)) * p.hg_max + h; };
         for (int h = wv; h < hg; h += kWorkersPerGroup) {
           const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
           float big_m = -INFINITY;
           for (int64_t base = 0; base < nc; base += kWave) {
             const int64_t j = base + lane;
-            const float m = j < nc ? p.part_ml[slot_of(v0 + j, h) * 2] : -INFINITY;
+            const float m = j < nc ? p.part_ml[slot_j(j, h) * 2] : -INFINITY;
             big_m = fmaxf(big_m, m);
           }
 #pragma unroll
           for (int off = 1; off < kWave; off <<= 1) big_m = fmaxf(big_m, shfl_xor(big_m, off));
           const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
 
-          float lsum = 0.f;
-          float acc[kPer];
+          float lsum = 0.f;  // this row group's share
+          float acc[8];
 #pragma unroll
-          for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
-          for (int64_t base = 0; base < nc; base += kWave) {
-            const int64_t j = base + lane;
-            float wgt = 0.f;
-            if (j < nc) {
-              const int64_t sl = slot_of(v0 + j, h);
-              wgt = __builtin_amdgcn_exp2f(p.part_ml[sl * 2] - base_m) * p.part_ml[sl * 2 + 1];
-              lsum += wgt;
+          for (int e8 = 0; e8 < 8; ++e8) acc[e8] = 0.f;
+          for (int64_t c0 = 0; c0 < nc; c0 += static_cast<int64_t>(kRpi) * kBatch) {
+            u32x4 ob[kBatch];
+            float mb[kBatch], lb[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+              const int64_t j = c0 + static_cast<int64_t>(u) * kRpi + rg;
+              const bool live = j < nc;
+              const int64_t sl = slot_j(live ? j : nc - 1, h);  // padding re-reads the last row
+              mb[u] = p.part_ml[sl * 2];
+              lb[u] = live ? p.part_ml[sl * 2 + 1] : 0.f;
+              ob[u] = dl ? *reinterpret_cast<const u32x4*>(p.part_o + sl * HD + rl * 8) : u32x4{0u, 0u, 0u, 0u};
             }
-            const int cnt = static_cast<int>((nc - base) < kWave ? (nc - base) : kWave);
-            // kBatch contributors' O loads in flight at a time (a load per
-            // contributor and a wait each would make the merge of a long
-            // sequence split into many chunks a chain of round trips)
-            for (int jj0 = 0; jj0 < cnt; jj0 += kBatch) {
-              uint16_t ob[kBatch][kPer];
 #pragma unroll
-              for (int u = 0; u < kBatch; ++u) {
-                const int jj = jj0 + u < cnt ? jj0 + u : cnt - 1;  // padding re-reads the last one
-                const uint16_t* o = p.part_o + slot_of(v0 + base + jj, h) * HD;
+            for (int u = 0; u < kBatch; ++u) {
+              const float w = __builtin_amdgcn_exp2f(mb[u] - base_m) * lb[u];
+              lsum += w;
 #pragma unroll
-                for (int q = 0; q < kPer; ++q) {
-                  const int d = lane + q * kWave;
-                  ob[u][q] = d < HD ? o[d] : uint16_t{0};
-                }
-              }
-#pragma unroll
-              for (int u = 0; u < kBatch; ++u) {
-                const float wj = jj0 + u < cnt ? __shfl(wgt, jj0 + u, kWave) : 0.f;
-#pragma unroll
-                for (int q = 0; q < kPer; ++q) acc[q] += wj * Dt<DT>::to_f32(ob[u][q]);
+              for (int e8 = 0; e8 < 8; ++e8) {
+                const uint32_t word = ob[u][e8 >> 1];
+                acc[e8] += w * Dt<DT>::to_f32(static_cast<uint16_t>((e8 & 1) ? (word >> 16) : (word & 0xFFFFu)));
               }
             }
           }
+          // combine the row groups (lanes kLpr, 2 kLpr, ... apart)
 #pragma unroll
-          for (int off = 1; off < kWave; off <<= 1) lsum += shfl_xor(lsum, off);
+          for (int off = kLpr; off < kWave; off <<= 1) {
+            lsum += shfl_xor(lsum, off);
+#pragma unroll
+            for (int e8 = 0; e8 < 8; ++e8) acc[e8] += shfl_xor(acc[e8], off);
+          }
           const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-#pragma unroll
-          for (int q = 0; q < kPer; ++q) {
-            const int d = lane + q * kWave;
-            if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
+          if (rg == 0 && dl) {  // out is 8-byte aligned: two 8-byte stores
+            uint16_t* dst = p.out + row * HD + rl * 8;
+            const u32x2 lo = {Dt<DT>::pack2(acc[0] * inv, acc[1] * inv), Dt<DT>::pack2(acc[2] * inv, acc[3] * inv)};
+            const u32x2 hi = {Dt<DT>::pack2(acc[4] * inv, acc[5] * inv), Dt<DT>::pack2(acc[6] * inv, acc[7] * inv)};
+            *reinterpret_cast<u32x2*>(dst) = lo;
+            *reinterpret_cast<u32x2*>(dst + 4) = hi;
           }
         }
       }
