@@ -216,28 +216,40 @@ struct ItemLds {
   const int32_t* seq;
 };
 
-// Streams the blocks of virtual worker v (one wavefront), with the loads of
-// PF blocks in flight ahead of the one being computed.  The range is a run
-// of pieces (the blocks of one segment inside the range); the pipeline runs
-// through piece boundaries: while the last blocks of a piece are computed,
+// Streams the blocks of virtual workers v_begin .. v_end-1 (one wavefront;
+// consecutive virtual workers own consecutive block ranges), with the loads
+// of PF blocks in flight ahead of the one being computed.  The blocks form a
+// run of pieces (the blocks of one segment inside one virtual worker's
+// range); the pipeline runs through piece boundaries, including those
+// between virtual workers: while the last blocks of a piece are computed,
 // the first blocks of the next piece are already loading (its item, query
 // and first page ids were fetched when the piece before it started).
-template <int DT, int HD, int TPP, int PF>
+template <int DT, int HD, int TPP, int PF, bool kMultiV>
 __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched& sc, const int64_t* cum,
-                                              const ItemLds il, int64_t n_items, int64_t v) {
+                                              const ItemLds il, int64_t n_items, int64_t v_begin,
+                                              int64_t v_end) {
   constexpr bool kK32 = (HD % 32) == 0;  // QK k-step of 32 (else 16)
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
   constexpr int NT = HD / 16;            // output tiles of 16 dims
   constexpr int NBUF = PF + 1;
 
-  const int64_t b0 = vstart(sc, v);
-  const int64_t range_end = vstart(sc, v + 1);
-  // merge-list slot of this virtual worker: written exactly once per call
-  // (the split segment whose first piece ends this range, or 0), so the slot
-  // never depends on what an earlier call left in the workspace
+  const int64_t b0 = vstart(sc, v_begin);
+  const int64_t b_end = vstart(sc, v_end);
+  // merge-list slot of each virtual worker: written exactly once per call
+  // (the split segment whose first piece ends its range, or none), so the
+  // slot never depends on what an earlier call left in the workspace
   int64_t list_g0 = -1, list_nb = 0, list_row = 0, list_seg = 0;  // g0 < 0: nothing to merge
-  if (range_end - b0 <= 0) {
-    if (lane_id() == 0 && v < p.list_cap) p.split_list[4 * v] = -1;
+  auto write_list = [&](int64_t v) {
+    if (lane_id() == 0 && v < p.list_cap) {
+      int64_t* slot = p.split_list + 4 * v;
+      slot[0] = list_g0;
+      slot[1] = list_nb;
+      slot[2] = list_row;
+      slot[3] = list_seg;
+    }
+  };
+  if (b_end - b0 <= 0) {
+    for (int64_t v = v_begin; v < v_end; ++v) write_list(v);
     return;
   }
 
@@ -250,8 +262,9 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 
   // A piece: item s (query row s of page-table row `seq`, `len` keys, nb
   // blocks per segment), segment `seg`, blocks [blk, blk + count) of the
-  // segment, starting at global block gpos; r = block offset of the piece
-  // inside the item's segments.  c_* is the piece being computed, x_* the
+  // segment, starting at global block gpos and ending at the latest at END
+  // (its virtual worker's range end); r = block offset of the piece inside
+  // the item's segments.  c_* is the piece being computed, x_* the
   // next one (kept in scalars: the pipeline state must stay in registers).
   int64_t c_s, c_r, c_gpos, c_seq, c_len, c_nb, c_blk, c_count;
   int c_seg;
@@ -259,7 +272,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   int x_seg;
   // the piece at item s, offset r, global block gpos (items with no key
   // have no blocks and are skipped)
-#define PAL_FIND_PIECE(P, S0, R0, G0)                                                              \
+#define PAL_FIND_PIECE(P, S0, R0, G0, END)                                                         \
   do {                                                                                             \
     int64_t s_ = (S0), r_ = (R0), len_, seq_;                                                      \
     for (;;) {                                                                                     \
@@ -283,7 +296,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     P##nb = (len_ + 15) >> 4;                                                                      \
     P##seg = static_cast<int>(r_ / P##nb);                                                         \
     P##blk = r_ - P##seg * P##nb;                                                                  \
-    P##count = (P##nb - P##blk) < (range_end - P##gpos) ? (P##nb - P##blk) : (range_end - P##gpos); \
+    P##count = (P##nb - P##blk) < ((END) - P##gpos) ? (P##nb - P##blk) : ((END) - P##gpos);         \
   } while (0)
 
   // Q^T operand of a piece: lane holds Q[head r16][k-slice of this lane]
@@ -314,9 +327,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     return pt[lp];
   };
 
+  int64_t c_v = v_begin, c_vend = vstart(sc, v_begin + 1);  // virtual worker of the piece, its range end
+  int64_t x_v = c_v, x_vend = c_vend;
   {
     const int64_t s0 = locate_seq(cum, n_items, b0);  // the item holding block b0 (it has blocks)
-    PAL_FIND_PIECE(c_, s0, b0 - cum[s0], b0);
+    PAL_FIND_PIECE(c_, s0, b0 - cum[s0], b0, c_vend);
   }
   load_q(c_s, c_seg, qv4, qv2);
 
@@ -337,7 +352,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   u32x2 vb[NBUF][NT];
   bool bv[NBUF];
 
-  bool first = true;
+  bool first = true;     // the piece is its virtual worker's first
+  bool prologue = true;  // the pipeline is empty
   bool has_next = false;
   x_s = c_s; x_r = c_r; x_gpos = c_gpos; x_seq = c_seq; x_len = c_len; x_nb = c_nb; x_blk = c_blk;
   x_count = c_count; x_seg = c_seg;
@@ -359,11 +375,13 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     const uint16_t* kbase_n = kbase;  // set once the next piece is known
     const uint16_t* vbase_n = vbase;
     int64_t nblk_n = 1;
+    int64_t bstart_n = 0, pbase_n = 0;  // first block of the next piece and its page index
 
     // Issue the K and V loads of step i of the piece into buffer `buf`:
     // block i of the piece (clamped to its last block), or, past the
-    // piece's steps, block i - n_pad of the next piece (which starts at
-    // block 0 of its segment).  An out-of-range page id is replaced by page
+    // piece's steps, block i - n_pad of the next piece (counted from its
+    // first block bstart_n: block 0 of its segment, or a chunk boundary in
+    // the fixed-chunk mode).  An out-of-range page id is replaced by page
     // 0 (in bounds) and the block is masked out when computed.  Every K/V
     // block is read exactly once per call, so the loads carry the
     // non-temporal hint: the stream does not displace other lines (page ids,
@@ -371,8 +389,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     auto issue = [&](int64_t i, int buf) {
       const bool to_next = has_next && i >= n_pad;
       const int64_t j = to_next ? (i - n_pad < nblk_n - 1 ? i - n_pad : nblk_n - 1) : (i < n_blk - 1 ? i : n_blk - 1);
-      const int64_t b = (to_next ? 0 : bstart) + j;
-      const int64_t e = (b * 16) / TPP - (to_next ? 0 : pbase);  // page of the piece
+      const int64_t b = (to_next ? bstart_n : bstart) + j;
+      const int64_t e = (b * 16) / TPP - (to_next ? pbase_n : pbase);  // page within the piece's windows
       // (selects of values, not of variables: a select of two variables'
       // addresses would push the whole pipeline state to scratch)
       const uint32_t w_n0 = pidn0, w_c = pid_cur, w_x = pid_nxt;
@@ -460,7 +478,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 
     // The first piece fills the pipeline; a later piece finds its first PF
     // blocks in flight already.
-    if (first) {
+    if (prologue) {
 #pragma unroll
       for (int q = 0; q < PF; ++q) issue(q, q);
     }
@@ -470,14 +488,22 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     // again, so these loads are unconditional.)
     {
       const int64_t gpos_n = c_gpos + c_count;
-      has_next = gpos_n < range_end;
+      has_next = gpos_n < b_end;
       int64_t s_n = c_s, r_n = c_r + c_count;
       if (r_n >= c_nb * segs) {
         ++s_n;
         r_n = 0;
       }
+      x_v = c_v;
+      x_vend = c_vend;
+      if constexpr (kMultiV) {
+        if (has_next && gpos_n >= c_vend) {  // the next piece is the next virtual worker's first
+          x_v = c_v + 1;
+          x_vend = vstart(sc, x_v + 1);
+        }
+      }
       if (has_next) {
-        PAL_FIND_PIECE(x_, s_n, r_n, gpos_n);
+        PAL_FIND_PIECE(x_, s_n, r_n, gpos_n, x_vend);
       } else {
         x_s = c_s; x_r = c_r; x_gpos = c_gpos; x_seq = c_seq; x_len = c_len; x_nb = c_nb; x_blk = c_blk;
         x_count = c_count; x_seg = c_seg;
@@ -491,6 +517,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       kbase_n = p.k_pool + kvh_x * head_block;
       vbase_n = p.v_pool + kvh_x * head_block;
       nblk_n = x_count;
+      bstart_n = x_blk;
+      pbase_n = (x_blk * 16) / TPP;
     }
 
     // Every step issues and computes unconditionally (steps past the end
@@ -545,7 +573,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
         // partial: (max, exp-sum) in fp32 and O / exp-sum in the 16-bit
         // dtype (half the bytes of fp32 O; the rounding is that of one more
         // output store)
-        const int64_t slot = (v * 2 + (first ? 0 : 1)) * p.hg_max + r16;
+        const int64_t slot = (c_v * 2 + (first ? 0 : 1)) * p.hg_max + r16;
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
@@ -559,16 +587,28 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       }
     }
 
-    // the first piece of a split segment can only end the range (a range
-    // ends inside one segment): that segment goes on the merge list
+    // the first piece of a split segment can only end a virtual worker's
+    // range (a range ends inside one segment): that segment goes on the
+    // worker's merge-list slot
     if (!complete && c_blk == 0) {
       list_g0 = c_gpos;  // the piece starts the segment
       list_nb = c_nb;
       list_row = c_s;
       list_seg = c_seg;
     }
+    prologue = false;
     first = false;
     if (!has_next) break;
+    if constexpr (kMultiV) {
+      if (x_v != c_v) {  // leaving virtual worker c_v
+        write_list(c_v);
+        list_g0 = -1;
+        list_nb = list_row = list_seg = 0;
+        first = true;
+        c_v = x_v;
+        c_vend = x_vend;
+      }
+    }
 
     // the next piece becomes current: its first PF blocks are in flight,
     // in buffers 0 .. PF-1 (n_pad is a multiple of NBUF)
@@ -583,17 +623,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     pid_nxt = pidn1;
     pid_later = load_window(c_seq, c_blk, 2);
   }
-  if (lane_id() == 0 && v < p.list_cap) {
-    int64_t* slot = p.split_list + 4 * v;
-    slot[0] = list_g0;
-    slot[1] = list_nb;
-    slot[2] = list_row;
-    slot[3] = list_seg;
-  }
+  write_list(c_v);
 #undef PAL_FIND_PIECE
 }
 
-template <int DT, int HD, int TPP, int PF>
+template <int DT, int HD, int TPP, int PF, bool kChunks>
 __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_lds, int64_t* len_lds,
                                             int32_t* seq_lds, int64_t* wave_sums) {
   const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
@@ -645,26 +679,39 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
   const ItemLds il = lds_plan ? ItemLds{len_lds, seq_lds} : ItemLds{nullptr, nullptr};
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
   const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
-  if (w < sc.nws) process_range<DT, HD, TPP, PF>(p, sc, cum, il, n_items, w);
-  while (sc.nc > 0) {
-    uint32_t k = 0;
-    if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
-    k = __builtin_amdgcn_readfirstlane(k);
-    if (k >= sc.nc) break;
-    process_range<DT, HD, TPP, PF>(p, sc, cum, il, n_items, sc.nws + k);
+  if constexpr (kChunks) {
+    // fixed chunks: wavefront w streams the run of consecutive chunks
+    // [w nc / W, (w + 1) nc / W) with one unbroken pipeline; each chunk is
+    // still its own virtual worker (its own partials and merge-list slot)
+    const int64_t nw = p.num_workers;
+    const int64_t va = w * sc.nc / nw, vb = (w + 1) * sc.nc / nw;
+    if (va < vb) process_range<DT, HD, TPP, PF, true>(p, sc, cum, il, n_items, va, vb);
+  } else {
+    if (w < sc.nws) process_range<DT, HD, TPP, PF, false>(p, sc, cum, il, n_items, w, w + 1);
+    if constexpr (kStaticShareNum < kStaticShareDen) {  // a dynamically claimed tail is compiled in
+      while (sc.nc > 0) {
+        uint32_t k = 0;
+        if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
+        k = __builtin_amdgcn_readfirstlane(k);
+        if (k >= sc.nc) break;
+        process_range<DT, HD, TPP, PF, false>(p, sc, cum, il, n_items, sc.nws + k, sc.nws + k + 1);
+      }
+    }
   }
 }
 
 // Plain decode: the whole GPU streams KV, one wavefront per SIMD.  (With
 // the non-temporal loads a third block of prefetch, or two wavefronts per
-// SIMD, measured slower.)
-template <int DT, int HD, int TPP>
+// SIMD, measured slower.)  kChunks: the fixed-chunk mode (partition_size >
+// 0), a separate instantiation so the equal-share kernel keeps its lower
+// register count.
+template <int DT, int HD, int TPP, bool kChunks>
 __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const DecodeParams p) {
   __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
   __shared__ int64_t len_lds[kInlinePlanSeqs];
   __shared__ int32_t seq_lds[kInlinePlanSeqs];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, kPrefetch>(p, cum_lds, len_lds, seq_lds, wave_sums);
+  stream_body<DT, HD, TPP, kPrefetch, kChunks>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Decode rows of the fused op: one workgroup per CU, held to half of the
@@ -688,7 +735,7 @@ void decode_shared_cu_kernel(const DecodeParams p) {
   __shared__ int64_t len_lds[kInlinePlanSeqs];
   __shared__ int32_t seq_lds[kInlinePlanSeqs];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>()>(p, cum_lds, len_lds, seq_lds, wave_sums);
+  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), false>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Walks the merge list, slot v for virtual worker v (first block < 0:
@@ -898,8 +945,11 @@ hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t st
       plain = false;
     }
   }
-  if (plain)
-    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)),
+  if (plain && p.tokens_per_worker > 0)
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, true>), dim3(static_cast<unsigned>(groups)),
+                       dim3(kGroupThreads), 0, stream, p);
+  else if (plain)
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, false>), dim3(static_cast<unsigned>(groups)),
                        dim3(kGroupThreads), 0, stream, p);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -938,27 +988,29 @@ hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, bool shared_cu, h
 }
 
 template <int DT, int HD, int TPP>
-const void* stream_kernel_ptr() {
-  return reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP>);
+const void* stream_kernel_ptr(bool chunks) {
+  return chunks ? reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP, true>)
+                : reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP, false>);
 }
 
 template <int DT>
-const void* stream_kernel_for(int hd, int tpp) {
+const void* stream_kernel_for(int hd, int tpp, bool chunks) {
   const bool t32 = tpp == 32;
   switch (hd) {
-    case 32: return t32 ? stream_kernel_ptr<DT, 32, 32>() : stream_kernel_ptr<DT, 32, 16>();
-    case 64: return t32 ? stream_kernel_ptr<DT, 64, 32>() : stream_kernel_ptr<DT, 64, 16>();
-    case 80: return t32 ? stream_kernel_ptr<DT, 80, 32>() : stream_kernel_ptr<DT, 80, 16>();
-    case 96: return t32 ? stream_kernel_ptr<DT, 96, 32>() : stream_kernel_ptr<DT, 96, 16>();
-    case 128: return t32 ? stream_kernel_ptr<DT, 128, 32>() : stream_kernel_ptr<DT, 128, 16>();
-    case 256: return t32 ? stream_kernel_ptr<DT, 256, 32>() : stream_kernel_ptr<DT, 256, 16>();
+    case 32: return t32 ? stream_kernel_ptr<DT, 32, 32>(chunks) : stream_kernel_ptr<DT, 32, 16>(chunks);
+    case 64: return t32 ? stream_kernel_ptr<DT, 64, 32>(chunks) : stream_kernel_ptr<DT, 64, 16>(chunks);
+    case 80: return t32 ? stream_kernel_ptr<DT, 80, 32>(chunks) : stream_kernel_ptr<DT, 80, 16>(chunks);
+    case 96: return t32 ? stream_kernel_ptr<DT, 96, 32>(chunks) : stream_kernel_ptr<DT, 96, 16>(chunks);
+    case 128: return t32 ? stream_kernel_ptr<DT, 128, 32>(chunks) : stream_kernel_ptr<DT, 128, 16>(chunks);
+    case 256: return t32 ? stream_kernel_ptr<DT, 256, 32>(chunks) : stream_kernel_ptr<DT, 256, 16>(chunks);
     default: return nullptr;
   }
 }
 
 }  // namespace
 
-hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, int* workers) {
+hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, bool chunks,
+                                   int* workers) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
@@ -969,8 +1021,8 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
     *workers = cus * kWorkersPerGroup;
     return hipSuccess;
   }
-  const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page)
-                                  : stream_kernel_for<kF16>(head_dim, tokens_per_page);
+  const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page, chunks)
+                                  : stream_kernel_for<kF16>(head_dim, tokens_per_page, chunks);
   if (!fn) return hipErrorInvalidValue;
   int groups_per_cu = 0;
   err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kGroupThreads, 0);

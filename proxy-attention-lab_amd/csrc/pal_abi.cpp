@@ -97,7 +97,8 @@ int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seq
                    int head_chunks, int64_t page_table_width, int partition_size, bool shared_cu, int* resident,
                    int64_t* virtual_workers) {
   int res = 0;
-  hipError_t err = pal::decode_resident_workers(dtype, head_dim, tokens_per_page, shared_cu, &res);
+  hipError_t err =
+      pal::decode_resident_workers(dtype, head_dim, tokens_per_page, shared_cu, partition_size > 0, &res);
   if (err != hipSuccess)
     return fail(PAL_ERR_HIP, "[paged_attention_decode] occupancy query failed: %s", hipGetErrorString(err));
   int64_t vw;

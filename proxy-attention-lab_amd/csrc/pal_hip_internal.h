@@ -72,8 +72,10 @@ struct DecodeParams {
 };
 
 // Workers the GPU keeps resident for this kernel configuration (shared_cu:
-// the fused op's decode, one workgroup per CU beside the prefill tiles).
-hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, int* workers);
+// the fused op's decode, one workgroup per CU beside the prefill tiles;
+// chunks: the fixed-chunk mode, partition_size > 0).
+hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, bool chunks,
+                                   int* workers);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
                          hipStream_t stream);
 
