@@ -711,7 +711,11 @@ __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const Deco
   __shared__ int64_t len_lds[kInlinePlanSeqs];
   __shared__ int32_t seq_lds[kInlinePlanSeqs];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, kPrefetch, kChunks>(p, cum_lds, len_lds, seq_lds, wave_sums);
+  // Fixed chunks are 8, 16 or 32 blocks: three blocks of prefetch make the
+  // steps of a chunk a whole number of step groups (no padded step per
+  // chunk; measured 2 % faster in the 512-token mode of config 3).
+  constexpr int kPf = kChunks && HD <= 128 ? kPrefetch + 1 : kPrefetch;  // (head_dim 256 would spill)
+  stream_body<DT, HD, TPP, kPf, kChunks>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Decode rows of the fused op: one workgroup per CU, held to half of the
