@@ -1,8 +1,8 @@
 // Paged-attention decode for gfx950: the KV stream of the whole batch is split
 // into 16-token blocks, shared out to a resident set of wavefront workers
-// (equal static shares, or fixed chunks claimed from a counter when a
-// partition size is given), and the pieces of sequences that several workers shared are merged with a
-// log-sum-exp pass.
+// (equal static shares, or static runs of fixed chunks when a partition size
+// is given), and the pieces of sequences that several workers shared are
+// merged with a log-sum-exp pass.
 //
 // Reference behaviour: kernels/paged_attention/decode/paged_attention_decode.h.metal
 // (one query row per sequence, GQA map h -> h / (Hq/Hkv) at :64-65, scale
@@ -15,11 +15,12 @@
 //    All query heads sharing a kv head (up to 16 per chunk) are processed
 //    together, so a K/V page block is read from HBM once per GQA group.
 //  * The global block list [0, T) is cut into "virtual workers": equal
-//    static ranges (one per resident wavefront) and, in the fixed-chunk mode
-//    (partition_size > 0) or when a static share below 1 is compiled in,
-//    chunks of C blocks that wavefronts claim from an atomic counter once
-//    their static range is done.  Because the cut is fixed, which wavefront
-//    computes a chunk changes nothing in the result.
+//    static ranges (one per resident wavefront), or, in the fixed-chunk mode
+//    (partition_size > 0), chunks of C blocks, each wavefront streaming a
+//    static run of consecutive chunks (when a static share below 1 is
+//    compiled in, a tail of chunks is claimed from an atomic counter
+//    instead).  Because the cut is fixed, which wavefront computes a chunk
+//    changes nothing in the result.
 //  * Each workgroup scans the sequence lengths into LDS (batches of up to
 //    1024 sequences; larger ones are scanned once by decode_plan_kernel into
 //    the workspace) and locates the sequence of a range by binary search.
@@ -104,8 +105,8 @@ struct Sched {
   int64_t total;  // T: blocks of all segments
   int64_t ts;     // static region [0, ts), split evenly over nws workers
   int64_t nws;    // static virtual workers: min(resident workers, ts), so none is empty
-  int64_t chunk;  // blocks per dynamic chunk
-  int64_t nc;     // dynamic chunks covering [ts, total); virtual ids nws .. nws + nc - 1
+  int64_t chunk;  // blocks per chunk
+  int64_t nc;     // chunks covering [ts, total); virtual ids nws .. nws + nc - 1
 };
 
 __device__ __forceinline__ Sched make_sched(int64_t total, int64_t nw, int tokens_per_worker) {
@@ -117,8 +118,8 @@ __device__ __forceinline__ Sched make_sched(int64_t total, int64_t nw, int token
   } else {
     // Static shares only.  (A dynamically claimed tail would absorb the
     // uneven finish of the shares, but each claimed range restarts the load
-    // pipeline; until ranges are chained without that bubble, small chunks
-    // cost more than they balance.)
+    // pipeline and writes its own partials; small chunks cost more than
+    // they balance.)
     sc.ts = total * kStaticShareNum / kStaticShareDen;
     const int64_t dyn = total - sc.ts;
     sc.chunk = (dyn + 4 * nw - 1) / (4 * nw);  // about four chunks per worker
