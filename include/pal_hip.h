@@ -93,8 +93,9 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
  * number of wavefront workers the device keeps resident.
  * partition_size: 0 (default: the KV blocks of the batch are cut into one
  * equal share per resident worker) or 128 / 256 / 512: fixed chunks of that
- * many tokens, claimed by whichever worker is free and merged by log-sum-exp
- * (the reference's CHUNK_SIZE is 512, paged_attention_types.h:33).
+ * many tokens, each worker streaming an equal run of consecutive chunks,
+ * every chunk its own partial, merged by log-sum-exp (the reference's
+ * CHUNK_SIZE is 512, paged_attention_types.h:33).
  * The workspace must be zero-filled before its first use; each call leaves
  * it ready for the next one on the same stream.
  */

@@ -156,9 +156,10 @@ def paged_attention_decode(
     the "[N*Hq, HD]" in the reference docstring does not match its code).
     ``partition_size`` (keyword-only): 0 shares the KV blocks of the batch
     out to the workers the GPU keeps resident, one equal share each; 128, 256
-    or 512 splits the KV stream into fixed chunks of that many tokens instead,
-    claimed by whichever worker is free; sequences split between workers are
-    merged by log-sum-exp as in the reference's two-pass mode.
+    or 512 splits the KV stream into fixed chunks of that many tokens instead
+    (each worker streams an equal run of consecutive chunks, every chunk its
+    own partial); partials are merged by log-sum-exp as in the reference's
+    two-pass mode.
     """
     op = "paged_attention_decode"
     _require_device("queries", queries)
