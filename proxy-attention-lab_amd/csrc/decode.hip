@@ -96,10 +96,6 @@ __device__ __forceinline__ Item item_at(const DecodeParams& p, int64_t i, int tp
   return it;
 }
 
-__device__ __forceinline__ int64_t seq_blocks(const DecodeParams& p, int64_t s, int tpp) {
-  return (item_at(p, s, tpp).len + 15) >> 4;
-}
-
 // The fixed cut of the global block list into virtual workers.
 struct Sched {
   int64_t total;  // T: blocks of all segments
