@@ -108,6 +108,15 @@ struct Sched {
 __device__ __forceinline__ Sched make_sched(int64_t total, int64_t nw, int tokens_per_worker) {
   Sched sc;
   sc.total = total;
+  if constexpr (kStaticShareNum == kStaticShareDen) {
+    if (tokens_per_worker <= 0) {  // equal shares only: no division on the start-up path
+      sc.ts = total;
+      sc.chunk = 1;
+      sc.nws = total < nw ? total : nw;
+      sc.nc = 0;
+      return sc;
+    }
+  }
   if (tokens_per_worker > 0) {  // fixed-size chunks only (the reference's CHUNK_SIZE mode)
     sc.ts = 0;
     sc.chunk = tokens_per_worker / 16 > 0 ? tokens_per_worker / 16 : 1;
