@@ -45,6 +45,9 @@
 //    virtual worker, combined by decode_merge_kernel.  The worker holding the
 //    first piece of a split segment writes it into its own slot of a merge
 //    list, so the merge grid does not grow with the batch.
+#include <mutex>
+#include <unordered_map>
+
 #include "pal_device.h"
 
 namespace pal {
@@ -1024,22 +1027,53 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
+  // The answer depends only on the device and the kernel instance: it is
+  // computed once (an occupancy query and an attribute read) and cached.
+  const bool shared = shared_cu && shares_cu(head_dim);
+  const uint64_t key = (static_cast<uint64_t>(dev) << 32) | (static_cast<uint64_t>(dtype & 0xff) << 24) |
+                       (static_cast<uint64_t>(head_dim & 0xfff) << 12) | (static_cast<uint64_t>(tokens_per_page & 0xff) << 4) |
+                       (shared ? 2u : 0u) | (chunks ? 1u : 0u);
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, int> cache;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) {
+      *workers = it->second;
+      return hipSuccess;
+    }
+  }
   int cus = 0;
   err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (err != hipSuccess) return err;
-  if (shared_cu && shares_cu(head_dim)) {  // one workgroup per CU; the prefill tiles take the rest
-    *workers = cus * kWorkersPerGroup;
-    return hipSuccess;
+  int res = 0;
+  if (shared) {  // one workgroup per CU; the prefill tiles take the rest
+    res = cus * kWorkersPerGroup;
+  } else {
+    const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page, chunks)
+                                    : stream_kernel_for<kF16>(head_dim, tokens_per_page, chunks);
+    if (!fn) return hipErrorInvalidValue;
+    int groups_per_cu = 0;
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kGroupThreads, 0);
+    if (err != hipSuccess) return err;
+    if (groups_per_cu < 1) groups_per_cu = 1;
+    res = cus * groups_per_cu * kWorkersPerGroup;
   }
-  const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page, chunks)
-                                  : stream_kernel_for<kF16>(head_dim, tokens_per_page, chunks);
-  if (!fn) return hipErrorInvalidValue;
-  int groups_per_cu = 0;
-  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kGroupThreads, 0);
-  if (err != hipSuccess) return err;
-  if (groups_per_cu < 1) groups_per_cu = 1;
-  *workers = cus * groups_per_cu * kWorkersPerGroup;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    cache[key] = res;
+  }
+  *workers = res;
   return hipSuccess;
+}
+
+int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partition_size) {
+  if (partition_size > 0) {  // one virtual worker per fixed chunk of the page-table capacity
+    const int64_t chunk = partition_size / 16;
+    return resident + (max_blocks + chunk - 1) / chunk;
+  }
+  if (kStaticShareNum == kStaticShareDen) return resident + 1;  // equal static shares only
+  return 5 * resident + 1;  // static shares plus about four claimed chunks per worker
 }
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,

@@ -90,9 +90,8 @@ DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t v
 }
 
 // Resident wavefront workers, and the number of virtual workers (partial
-// slots) the cut can produce: static shares plus at most four dynamic chunks
-// per worker, or, with a partition size, one chunk per partition of the
-// page-table capacity.
+// slots) the cut can produce: one per equal static share, or, with a
+// partition size, one per chunk of the page-table capacity.
 int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seqs, int num_kv_heads,
                    int head_chunks, int64_t page_table_width, int partition_size, bool shared_cu, int* resident,
                    int64_t* virtual_workers) {
@@ -101,15 +100,9 @@ int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seq
       pal::decode_resident_workers(dtype, head_dim, tokens_per_page, shared_cu, partition_size > 0, &res);
   if (err != hipSuccess)
     return fail(PAL_ERR_HIP, "[paged_attention_decode] occupancy query failed: %s", hipGetErrorString(err));
-  int64_t vw;
-  if (partition_size > 0) {
-    const int64_t max_blocks =
-        num_seqs * ((page_table_width * tokens_per_page + 15) / 16) * num_kv_heads * head_chunks;
-    const int64_t chunk = partition_size / 16;
-    vw = res + (max_blocks + chunk - 1) / chunk;
-  } else {
-    vw = 5LL * res + 1;
-  }
+  const int64_t max_blocks =
+      num_seqs * ((page_table_width * tokens_per_page + 15) / 16) * num_kv_heads * head_chunks;
+  const int64_t vw = pal::decode_virtual_workers(res, max_blocks, partition_size);
   if (vw > (1LL << 28)) return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] problem too large for one call");
   *resident = res;
   *virtual_workers = vw;
@@ -193,6 +186,61 @@ int check_attention_dims(const char* op, int dtype, int num_q_heads, int num_kv_
   if (tokens_per_page != 16 && tokens_per_page != 32)
     return fail(PAL_ERR_RUNTIME, "[%s] no kernel for tokens_per_page %d (supported: 16, 32)", op, tokens_per_page);
   return PAL_OK;
+}
+
+// pal_paged_attention_decode: validation, workspace check and launch.
+int decode_call(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
+                const int32_t* sequence_lengths, void* out, int dtype, int64_t num_query_rows, int64_t num_seqs,
+                int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                int64_t page_table_width, int partition_size, void* workspace, size_t workspace_bytes,
+                hipStream_t stream) {
+  if (!valid_dtype(dtype))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] unsupported dtype code %d", dtype);
+  if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
+      num_pages < 0 || page_table_width < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] negative or zero dimension");
+  if (num_q_heads % num_kv_heads != 0)
+    return fail(PAL_ERR_RUNTIME, "num_q_heads must be divisible by num_kv_heads (%d %% %d != 0)",
+                num_q_heads, num_kv_heads);
+  if (!decode_head_dim_supported(head_dim))
+    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for head_dim %d (supported: 32, 64, 80, 96, 128, 256)", head_dim);
+  if (tokens_per_page != 16 && tokens_per_page != 32)
+    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for tokens_per_page %d (supported: 16, 32)", tokens_per_page);
+  if (!decode_partition_ok(partition_size))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] partition_size %d not in {0, 128, 256, 512}",
+                partition_size);
+  if (num_query_rows < num_seqs)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] %lld query rows for %lld sequences",
+                static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs));
+  if (num_seqs == 0) return ok();
+  if (num_pages == 0) page_table_width = 0;  // no page to read: every sequence is empty
+  const int group = num_q_heads / num_kv_heads;
+  const int chunks = (group + 15) / 16;
+  const int hg_max = group < 16 ? group : 16;
+  int resident = 0;
+  int64_t vw = 0;
+  const int st = decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
+                                partition_size, false, &resident, &vw);
+  if (st != PAL_OK) return st;
+  const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, vw);
+  if (!queries || !sequence_lengths || !out || (num_pages > 0 && (!k_pool || !v_pool)) ||
+      (page_table_width > 0 && !page_table))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] null pointer argument");
+  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(PAL_ERR_INVALID_ARGUMENT,
+                "[paged_attention_decode] queries and pools must be 16-byte aligned, out 8-byte aligned");
+  if (workspace == nullptr || workspace_bytes < lay.total)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace of %zu bytes needed, %zu given",
+                lay.total, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 256-byte aligned");
+
+  const pal::DecodeParams p = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
+                                            static_cast<char*>(workspace), lay, num_seqs, num_pages,
+                                            page_table_width, num_q_heads, num_kv_heads, head_dim, resident,
+                                            partition_size);
+  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, false, stream),
+                    "paged_attention_decode");
 }
 
 }  // namespace
@@ -292,53 +340,9 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                int tokens_per_page, int64_t num_pages, int64_t page_table_width,
                                int partition_size, void* workspace, size_t workspace_bytes,
                                void* stream) {
-  if (!valid_dtype(dtype))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] unsupported dtype code %d", dtype);
-  if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
-      num_pages < 0 || page_table_width < 0)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] negative or zero dimension");
-  if (num_q_heads % num_kv_heads != 0)
-    return fail(PAL_ERR_RUNTIME, "num_q_heads must be divisible by num_kv_heads (%d %% %d != 0)",
-                num_q_heads, num_kv_heads);
-  if (!decode_head_dim_supported(head_dim))
-    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for head_dim %d (supported: 32, 64, 80, 96, 128, 256)", head_dim);
-  if (tokens_per_page != 16 && tokens_per_page != 32)
-    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no kernel for tokens_per_page %d (supported: 16, 32)", tokens_per_page);
-  if (!decode_partition_ok(partition_size))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] partition_size %d not in {0, 128, 256, 512}",
-                partition_size);
-  if (num_query_rows < num_seqs)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] %lld query rows for %lld sequences",
-                static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs));
-  if (num_seqs == 0) return ok();
-  if (num_pages == 0) page_table_width = 0;  // no page to read: every sequence is empty
-  if (!queries || !sequence_lengths || !out || (num_pages > 0 && (!k_pool || !v_pool)) ||
-      (page_table_width > 0 && !page_table))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] null pointer argument");
-  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fail(PAL_ERR_INVALID_ARGUMENT,
-                "[paged_attention_decode] queries and pools must be 16-byte aligned, out 8-byte aligned");
-  const int group = num_q_heads / num_kv_heads;
-  const int chunks = (group + 15) / 16;
-  const int hg_max = group < 16 ? group : 16;
-  int resident = 0;
-  int64_t vw = 0;
-  const int st = decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                                partition_size, false, &resident, &vw);
-  if (st != PAL_OK) return st;
-  const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, vw);
-  if (workspace == nullptr || workspace_bytes < lay.total)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace of %zu bytes needed, %zu given",
-                lay.total, workspace_bytes);
-  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 256-byte aligned");
-
-  const pal::DecodeParams p = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
-                                            static_cast<char*>(workspace), lay, num_seqs, num_pages,
-                                            page_table_width, num_q_heads, num_kv_heads, head_dim, resident,
-                                            partition_size);
-  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, false, static_cast<hipStream_t>(stream)),
-                    "paged_attention_decode");
+  return decode_call(queries, k_pool, v_pool, page_table, sequence_lengths, out, dtype, num_query_rows, num_seqs,
+                     num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages, page_table_width,
+                     partition_size, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, const void* v_prompt,

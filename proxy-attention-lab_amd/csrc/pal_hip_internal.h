@@ -76,6 +76,10 @@ struct DecodeParams {
 // chunks: the fixed-chunk mode, partition_size > 0).
 hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, bool chunks,
                                    int* workers);
+// Virtual workers (merge-list and partial slots) a call can produce: the
+// resident workers' equal shares, or, with a partition size, one per fixed
+// chunk of max_blocks (the 16-token blocks the page tables can hold).
+int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partition_size);
 hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
                          hipStream_t stream);
 

@@ -19,6 +19,8 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 from . import _lib
@@ -46,6 +48,21 @@ def _stream_handle(stream, device: torch.device) -> int:
     if isinstance(stream, int):
         return stream
     raise TypeError(f"stream must be None, a torch.cuda.Stream or an int handle, got {type(stream)!r}")
+
+
+def _on_stream(stream_handle: int, device: torch.device):
+    """Context in which torch work (index conversions, contiguous copies,
+    output and workspace allocation) is ordered on the launch stream.
+
+    The kernels run on ``stream_handle``; any temporary the call makes must
+    be written on that same stream, and the caching allocator must see it as
+    that stream's memory, or a kernel could read a half-written buffer or a
+    block freed and reused by another stream.  When the launch stream is
+    torch's current stream this is a no-op.
+    """
+    if stream_handle == torch.cuda.current_stream(device).cuda_stream:
+        return contextlib.nullcontext()
+    return torch.cuda.stream(torch.cuda.ExternalStream(stream_handle, device=device))
 
 
 def _require_device(name: str, t: torch.Tensor, device: torch.device | None = None) -> None:
@@ -90,9 +107,10 @@ def _workspace(kind: str, nbytes: int, device: torch.device, stream_handle: int)
     key = (kind, device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        # allocated and zero-filled on the launch stream (the caller holds
+        # _on_stream), so the buffer it replaces, still in use by kernels
+        # queued on that stream, is only reused after them
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        # the zero fill ran on torch's current stream; the kernels may use another
-        torch.cuda.current_stream(device).synchronize()
         _WORKSPACES[key] = ws
     return ws
 
@@ -170,29 +188,31 @@ def paged_attention_decode(
     if page_table.dim() != 2:
         raise ValueError("[paged_attention_decode] page_table must be 2D [num_seqs, max_pages_per_seq]")
     num_seqs, width = (int(x) for x in page_table.shape)
-    pt = _index_tensor("page_table", page_table, device)
-    lens = _index_tensor("sequence_lengths", sequence_lengths, device)
-    if lens.numel() < num_seqs:
-        raise ValueError(f"[paged_attention_decode] {lens.numel()} sequence lengths for {num_seqs} sequences")
-    q = queries.contiguous()
-    kp = k_cache_pool.contiguous()
-    vp = v_cache_pool.contiguous()
-    out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=queries.dtype, device=device)
+    _require_device("sequence_lengths", sequence_lengths, device)
+    if sequence_lengths.numel() < num_seqs:
+        raise ValueError(
+            f"[paged_attention_decode] {sequence_lengths.numel()} sequence lengths for {num_seqs} sequences")
     L = _lib.lib()
-    ws = None
-    ws_bytes = 0
     sh = _stream_handle(stream, device)
-    if num_seqs > 0:
-        with torch.cuda.device(device):
-            ws_bytes = L.pal_paged_attention_decode_workspace_size(
-                code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width, int(partition_size))
-        ws = _workspace("decode", ws_bytes, device, sh)
-    status = L.pal_paged_attention_decode(
-        _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
-        code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
-        num_pages, width, int(partition_size),
-        _ptr(ws), ws.numel() if ws is not None else 0, sh,
-    )
+    with _on_stream(sh, device):
+        pt = _index_tensor("page_table", page_table, device)
+        lens = _index_tensor("sequence_lengths", sequence_lengths, device)
+        q = queries.contiguous()
+        kp = k_cache_pool.contiguous()
+        vp = v_cache_pool.contiguous()
+        out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=queries.dtype, device=device)
+        ws = None
+        if num_seqs > 0:
+            with torch.cuda.device(device):
+                ws_bytes = L.pal_paged_attention_decode_workspace_size(
+                    code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width, int(partition_size))
+            ws = _workspace("decode", ws_bytes, device, sh)
+        status = L.pal_paged_attention_decode(
+            _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
+            code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
+            num_pages, width, int(partition_size),
+            _ptr(ws), ws.numel() if ws is not None else 0, sh,
+        )
     _lib.check(status)
     return out
 
@@ -241,9 +261,11 @@ def fill_kv_pages(
     if not global_key_pool.is_contiguous() or not global_value_pool.is_contiguous():
         raise ValueError("[fill_kv_pages] pools must be contiguous (they are updated in place)")
     n = int(new_keys.shape[0]) if new_keys.dim() > 0 else 0
+    sh = _stream_handle(stream, device)
     if copy:
-        global_key_pool = global_key_pool.clone()
-        global_value_pool = global_value_pool.clone()
+        with _on_stream(sh, device):
+            global_key_pool = global_key_pool.clone()
+            global_value_pool = global_value_pool.clone()
     if n == 0 or new_keys.numel() == 0:
         return global_key_pool, global_value_pool
     if tuple(new_keys.shape) != (n, num_kv_heads, head_dim) or tuple(new_values.shape) != (n, num_kv_heads, head_dim):
@@ -254,17 +276,18 @@ def fill_kv_pages(
     if page_table.dim() != 2:
         raise ValueError("[fill_kv_pages] page_table must be 2D")
     num_seqs, width = (int(x) for x in page_table.shape)
-    pt = _index_tensor("page_table", page_table, device)
-    pos = _index_tensor("current_token_write_positions", current_token_write_positions, device)
-    q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
-    if pos.numel() < n or q2s.numel() < n:
+    if current_token_write_positions.numel() < n or query_to_seq_map.numel() < n:
         raise ValueError("[fill_kv_pages] write positions and query_to_seq_map need one entry per new token")
-    nk = new_keys.contiguous()
-    nv = new_values.contiguous()
-    status = _lib.lib().pal_fill_kv_pages(
-        _ptr(nk), _ptr(nv), _ptr(global_key_pool), _ptr(global_value_pool), _ptr(pt), _ptr(pos), _ptr(q2s),
-        code, n, num_kv_heads, head_dim, tpp, num_pages, num_seqs, width, _stream_handle(stream, device),
-    )
+    with _on_stream(sh, device):
+        pt = _index_tensor("page_table", page_table, device)
+        pos = _index_tensor("current_token_write_positions", current_token_write_positions, device)
+        q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
+        nk = new_keys.contiguous()
+        nv = new_values.contiguous()
+        status = _lib.lib().pal_fill_kv_pages(
+            _ptr(nk), _ptr(nv), _ptr(global_key_pool), _ptr(global_value_pool), _ptr(pt), _ptr(pos), _ptr(q2s),
+            code, n, num_kv_heads, head_dim, tpp, num_pages, num_seqs, width, sh,
+        )
     _lib.check(status)
     return global_key_pool, global_value_pool
 
@@ -308,25 +331,26 @@ def paged_attention_prefill(
     if page_table.dim() != 2:
         raise ValueError(f"[{op}] page_table must be 2D [num_seqs, max_pages_per_seq]")
     num_seqs, width = (int(x) for x in page_table.shape)
-    pt = _index_tensor("page_table", page_table, device)
-    ctx = _index_tensor("context_len_arr", context_len_arr, device)
-    if ctx.numel() < num_seqs:
-        raise ValueError(f"[{op}] {ctx.numel()} context lengths for {num_seqs} sequences")
-    q = q_prompt.contiguous()
-    kd = k_prompt.contiguous()
-    vd = v_prompt.contiguous()
-    kp = k_cache_paged.contiguous()
-    vp = v_cache_paged.contiguous()
-    out = torch.empty((num_rows * num_q_heads, head_dim), dtype=q_prompt.dtype, device=device)
+    _require_device("context_len_arr", context_len_arr, device)
+    if context_len_arr.numel() < num_seqs:
+        raise ValueError(f"[{op}] {context_len_arr.numel()} context lengths for {num_seqs} sequences")
     covered = num_seqs * (num_rows // num_seqs) if num_seqs > 0 else 0
     sh = _stream_handle(stream, device)
-    if covered < num_rows:
-        with torch.cuda.stream(torch.cuda.ExternalStream(sh, device=device)):
+    with _on_stream(sh, device):
+        pt = _index_tensor("page_table", page_table, device)
+        ctx = _index_tensor("context_len_arr", context_len_arr, device)
+        q = q_prompt.contiguous()
+        kd = k_prompt.contiguous()
+        vd = v_prompt.contiguous()
+        kp = k_cache_paged.contiguous()
+        vp = v_cache_paged.contiguous()
+        out = torch.empty((num_rows * num_q_heads, head_dim), dtype=q_prompt.dtype, device=device)
+        if covered < num_rows:
             out[covered * num_q_heads:].zero_()
-    status = _lib.lib().pal_paged_attention_prefill(
-        _ptr(q), _ptr(kd), _ptr(vd), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(ctx), _ptr(out),
-        code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width, sh,
-    )
+        status = _lib.lib().pal_paged_attention_prefill(
+            _ptr(q), _ptr(kd), _ptr(vd), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(ctx), _ptr(out),
+            code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width, sh,
+        )
     _lib.check(status)
     return out
 
@@ -363,29 +387,34 @@ def paged_attention(
     if page_table.dim() != 2:
         raise ValueError(f"[{op}] page_table must be 2D [num_seqs, max_pages_per_seq]")
     num_seqs, width = (int(x) for x in page_table.shape)
-    pt = _index_tensor("page_table", page_table, device)
-    lens = _index_tensor("sequence_lengths", sequence_lengths, device)
-    q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
-    off = _index_tensor("query_token_offset", query_token_offset, device)
-    if lens.numel() < num_seqs:
-        raise ValueError(f"[{op}] {lens.numel()} sequence lengths for {num_seqs} sequences")
-    if q2s.numel() != num_rows or off.numel() != num_rows:
+    for name, t in (("sequence_lengths", sequence_lengths), ("query_to_seq_map", query_to_seq_map),
+                    ("query_token_offset", query_token_offset)):
+        _require_device(name, t, device)
+    if sequence_lengths.numel() < num_seqs:
+        raise ValueError(f"[{op}] {sequence_lengths.numel()} sequence lengths for {num_seqs} sequences")
+    if query_to_seq_map.numel() != num_rows or query_token_offset.numel() != num_rows:
         raise ValueError(f"[{op}] query_to_seq_map and query_token_offset need one entry per query row ({num_rows})")
-    q = queries.contiguous()
-    kp = k_cache_pool.contiguous()
-    vp = v_cache_pool.contiguous()
-    out = torch.empty((num_rows, num_q_heads, head_dim), dtype=queries.dtype, device=device)
     L = _lib.lib()
     sh = _stream_handle(stream, device)
-    ws = None
-    if num_rows > 0:
-        with torch.cuda.device(device):
-            ws_bytes = L.pal_paged_attention_workspace_size(code, num_rows, num_q_heads, num_kv_heads, head_dim, tpp)
-        ws = _workspace("fused", ws_bytes, device, sh)
-    status = L.pal_paged_attention(
-        _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(q2s), _ptr(off), _ptr(out),
-        code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width,
-        _ptr(ws), ws.numel() if ws is not None else 0, sh,
-    )
+    with _on_stream(sh, device):
+        pt = _index_tensor("page_table", page_table, device)
+        lens = _index_tensor("sequence_lengths", sequence_lengths, device)
+        q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
+        off = _index_tensor("query_token_offset", query_token_offset, device)
+        q = queries.contiguous()
+        kp = k_cache_pool.contiguous()
+        vp = v_cache_pool.contiguous()
+        out = torch.empty((num_rows, num_q_heads, head_dim), dtype=queries.dtype, device=device)
+        ws = None
+        if num_rows > 0:
+            with torch.cuda.device(device):
+                ws_bytes = L.pal_paged_attention_workspace_size(code, num_rows, num_q_heads, num_kv_heads, head_dim,
+                                                                tpp)
+            ws = _workspace("fused", ws_bytes, device, sh)
+        status = L.pal_paged_attention(
+            _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(q2s), _ptr(off), _ptr(out),
+            code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width,
+            _ptr(ws), ws.numel() if ws is not None else 0, sh,
+        )
     _lib.check(status)
     return out

@@ -113,16 +113,41 @@ def compact_subset(case: PagedCase, seqs) -> PagedCase:
                      case.k_pool[uniq], case.v_pool[uniq])
 
 
+def _log_margin(what: str, dtype: str, max_err: float, worst: float) -> None:
+    """Record how close a comparison came to its tolerance: max |err| and the
+    largest |err| / (atol + rtol |expected|) (below 1 passes).  Printed to the
+    real stderr (outside pytest's capture) and, if PAL_MARGIN_LOG names a
+    file, appended to it as one JSON line."""
+    import json
+    import os
+    import sys
+
+    tol = TOL[dtype]
+    rec = {"case": what, "dtype": dtype, "atol": tol["atol"], "rtol": tol["rtol"], "max_abs_err": max_err,
+           "worst_err_over_allowed": worst}
+    print(f"[margin] {what} {dtype}: max|err| {max_err:.3g}, worst err/allowed {worst:.3f} "
+          f"(atol {tol['atol']}, rtol {tol['rtol']})", file=sys.__stderr__, flush=True)
+    path = os.environ.get("PAL_MARGIN_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+
+
 def assert_close(actual_f32: np.ndarray, expected_f32: np.ndarray, dtype: str, what: str = "") -> None:
     tol = TOL[dtype]
     a = np.asarray(actual_f32, np.float32)
     e = np.asarray(expected_f32, np.float32)
     assert a.shape == e.shape, f"{what}: shape {a.shape} != {e.shape}"
     ok = np.isclose(a, e, atol=tol["atol"], rtol=tol["rtol"])
+    diff = np.abs(a.astype(np.float64) - e.astype(np.float64))
+    if a.size:
+        with np.errstate(invalid="ignore"):
+            ratio = diff / (tol["atol"] + tol["rtol"] * np.abs(e.astype(np.float64)))
+        _log_margin(what, dtype, float(np.nanmax(diff)) if np.isfinite(diff).any() else float("inf"),
+                    float(np.nanmax(ratio)) if np.isfinite(ratio).any() else float("inf"))
     if not ok.all():
         bad = np.argwhere(~ok)
         i = tuple(bad[0])
-        diff = np.abs(a - e)
         raise AssertionError(
             f"{what}: {len(bad)} of {a.size} elements outside atol={tol['atol']} rtol={tol['rtol']}; "
             f"max |diff| {np.nanmax(diff):.4g}; first at {i}: got {a[i]!r}, want {e[i]!r}"

@@ -103,12 +103,37 @@ def test_decode_two_dim_queries():
     assert_close(host_f32(out), ref, "f16")
 
 
-def test_decode_long_context_outliers():
-    """Config-3-like long contexts with 1% of key rows scaled x8, 512-token
-    partitions merged by the log-sum-exp pass."""
+@pytest.mark.parametrize("partition", [512, 0])
+def test_decode_long_context_outliers(partition):
+    """Config-3-like long contexts with 1% of key rows scaled x8: 512-token
+    partitions merged by the log-sum-exp pass, and the default equal shares."""
     case = make_paged_case(77, [40000, 70001], 32, 8, 128, 16, "bf16", outlier_frac=0.01)
     q = randn_bits(np.random.default_rng(77), (2, 32, 128), "bf16")
-    _check(case, q, 512, what="long-context")
+    _check(case, q, partition, what=f"long-context partition {partition}")
+
+
+@pytest.mark.parametrize("partition", [128, 512])
+@pytest.mark.parametrize("hd,dtype,tpp", [(256, "bf16", 16), (256, "f16", 32), (128, "f16", 16), (64, "f16", 32),
+                                          (80, "bf16", 16)])
+def test_decode_partition_modes(hd, dtype, tpp, partition):
+    """The fixed-chunk kernel instances: head_dim 256 (two blocks of
+    prefetch), fp16, 32-token pages, head dims that are not multiples of 32."""
+    lens = RAGGED_LENS + [5000, 1537]
+    case = make_paged_case(hd + tpp + partition, lens, 16, 4, hd, tpp, dtype)
+    q = randn_bits(np.random.default_rng(hd * 3 + partition), (len(lens), 16, hd), dtype)
+    _check(case, q, partition, what=f"partition {partition} hd{hd}")
+
+
+@pytest.mark.parametrize("partition", [128, 512])
+def test_decode_partition_many_sequences(partition):
+    """Fixed-chunk mode with more sequences than the in-kernel planner takes
+    (the separate plan kernel), zero lengths among them."""
+    rng = np.random.default_rng(17 + partition)
+    lens = rng.integers(0, 700, size=1300).astype(np.int32)
+    lens[rng.choice(1300, 50, replace=False)] = 0
+    case = make_paged_case(17, lens, 8, 2, 128, 16, "bf16")
+    q = randn_bits(rng, (1300, 8, 128), "bf16")
+    _check(case, q, partition, what=f"1300 sequences partition {partition}")
 
 
 def test_decode_deterministic():

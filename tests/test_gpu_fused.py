@@ -155,3 +155,13 @@ def test_fused_deterministic_and_empty():
                                 dev_bits(c.v_pool, "bf16"), dev_index(c.page_table), dev_index(c.seq_lens),
                                 dev_index(fc.q2seq[:0]), dev_index(fc.q_offset[:0]))
     assert empty.shape == (0, 32, 128)
+
+
+@pytest.mark.parametrize("tpp", [16, 32])
+def test_fused_long_history_window(tpp):
+    """A prefill run over a cache longer than 8192 keys (window mode stages
+    its page ids in chunks of 512 entries and rotates them), beside decode
+    rows of similar length."""
+    fc = make_fused_case(70 + tpp, [100, 30000], [(26000 if tpp == 16 else 38000, 64), (9000, 40)], 32, 8, 128,
+                         tpp, "bf16", block=64)
+    _check_fused(fc, f"long history window tpp{tpp}")

@@ -116,3 +116,12 @@ def test_prefill_deterministic():
     a = host_bits(_prefill_gpu(q, k, v, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "bf16"))
     b = host_bits(_prefill_gpu(q, k, v, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "bf16"))
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("tpp,hist", [(16, [26000, 9000]), (32, [40000, 300])])
+def test_prefill_long_history_page_id_chunks(tpp, hist):
+    """Histories longer than 8192 keys: the page ids of a tile are staged into
+    LDS in chunks of 512 entries, two live at a time; these cases need three
+    or four chunks, so the kernel stages later chunks over earlier ones while
+    the key loop runs."""
+    _check(31 + tpp, hist, 48, 32, 8, 128, tpp, "bf16", f"long history tpp{tpp}")
