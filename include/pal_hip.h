@@ -129,6 +129,24 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                void* stream);
 
 /*
+ * No counterpart in the reference.  The same operation as
+ * pal_paged_attention_decode for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): there is no workspace argument, and the call allocates nothing.
+ * Its scratch (the length scan, merge list and split partials) is a
+ * library-held device array of 64 MiB per GPU, kept until the process ends;
+ * shapes whose workspace (pal_paged_attention_decode_workspace_size) would
+ * exceed it are rejected with PAL_ERR_INVALID_ARGUMENT.  Every call on one
+ * GPU shares that GPU's array: calls that can overlap on one GPU (different
+ * streams, or threads) race and must be serialised by the caller.
+ */
+int pal_paged_attention_decode_noalloc(const void* queries, const void* k_pool, const void* v_pool,
+                                       const uint32_t* page_table, const int32_t* sequence_lengths, void* out,
+                                       int dtype, int64_t num_query_rows, int64_t num_seqs, int num_q_heads,
+                                       int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                                       int64_t page_table_width, int partition_size, void* stream);
+
+/*
  * Replaces paged_attention_prefill (ops.py:87-130 -> bindings.cpp:74-124 ->
  * ops.cpp:110-186 -> paged_attention_prefill_primitive.cpp:63-167).
  * num_seqs = page-table rows; prompt_len P = num_query_rows / num_seqs

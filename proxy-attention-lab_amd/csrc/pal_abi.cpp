@@ -188,12 +188,15 @@ int check_attention_dims(const char* op, int dtype, int num_q_heads, int num_kv_
   return PAL_OK;
 }
 
-// pal_paged_attention_decode: validation, workspace check and launch.
+// pal_paged_attention_decode and its no-allocation variant: with
+// use_scratch the workspace is the library's per-device scratch array (no
+// caller buffer, nothing allocated), and calls needing more than it holds
+// are rejected.
 int decode_call(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
                 const int32_t* sequence_lengths, void* out, int dtype, int64_t num_query_rows, int64_t num_seqs,
                 int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
                 int64_t page_table_width, int partition_size, void* workspace, size_t workspace_bytes,
-                hipStream_t stream) {
+                bool use_scratch, hipStream_t stream) {
   if (!valid_dtype(dtype))
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] unsupported dtype code %d", dtype);
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
@@ -223,12 +226,24 @@ int decode_call(const void* queries, const void* k_pool, const void* v_pool, con
                                 partition_size, false, &resident, &vw);
   if (st != PAL_OK) return st;
   const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, vw);
+  if (use_scratch) {
+    if (lay.total > pal::kScratchBytes)
+      return fail(PAL_ERR_INVALID_ARGUMENT,
+                  "[paged_attention_decode_noalloc] these shapes need %zu bytes of scratch; the library holds %zu "
+                  "per device (use pal_paged_attention_decode with a caller workspace)",
+                  lay.total, pal::kScratchBytes);
+  }
   if (!queries || !sequence_lengths || !out || (num_pages > 0 && (!k_pool || !v_pool)) ||
       (page_table_width > 0 && !page_table))
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] null pointer argument");
   if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(PAL_ERR_INVALID_ARGUMENT,
                 "[paged_attention_decode] queries and pools must be 16-byte aligned, out 8-byte aligned");
+  if (use_scratch) {
+    const hipError_t err = pal::scratch_buffer(&workspace);
+    if (err != hipSuccess) return hip_status(err, "paged_attention_decode_noalloc");
+    workspace_bytes = pal::kScratchBytes;
+  }
   if (workspace == nullptr || workspace_bytes < lay.total)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace of %zu bytes needed, %zu given",
                 lay.total, workspace_bytes);
@@ -342,7 +357,17 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                void* stream) {
   return decode_call(queries, k_pool, v_pool, page_table, sequence_lengths, out, dtype, num_query_rows, num_seqs,
                      num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages, page_table_width,
-                     partition_size, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                     partition_size, workspace, workspace_bytes, false, static_cast<hipStream_t>(stream));
+}
+
+int pal_paged_attention_decode_noalloc(const void* queries, const void* k_pool, const void* v_pool,
+                                       const uint32_t* page_table, const int32_t* sequence_lengths, void* out,
+                                       int dtype, int64_t num_query_rows, int64_t num_seqs, int num_q_heads,
+                                       int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                                       int64_t page_table_width, int partition_size, void* stream) {
+  return decode_call(queries, k_pool, v_pool, page_table, sequence_lengths, out, dtype, num_query_rows, num_seqs,
+                     num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages, page_table_width,
+                     partition_size, nullptr, 0, true, static_cast<hipStream_t>(stream));
 }
 
 int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, const void* v_prompt,

@@ -118,4 +118,10 @@ struct PrefillParams {
 int prefill_tokens_per_tile(int group);
 hipError_t launch_prefill(const PrefillParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
 
+// Scratch memory held by the library for pal_paged_attention_decode_noalloc:
+// kScratchBytes per device, in a file-scope device array (scratch.hip).
+// scratch_buffer returns its device address on the current device.
+constexpr size_t kScratchBytes = static_cast<size_t>(64) << 20;
+hipError_t scratch_buffer(void** ptr);
+
 }  // namespace pal

@@ -51,6 +51,12 @@ _SIGNATURES = {
         + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int]
         + [_c_void_p, _c_size_t, _c_void_p],
     ),
+    "pal_paged_attention_decode_noalloc": (
+        _c_int,
+        [_c_void_p] * 6
+        + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int]
+        + [_c_void_p],
+    ),
     "pal_paged_attention_prefill": (
         _c_int,
         [_c_void_p] * 8 + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_void_p],
