@@ -75,6 +75,24 @@ def paged_pool(rng: np.random.Generator, g: torch.Generator, lens: np.ndarray, h
     return k_pool, v_pool, pt
 
 
+def to_fp8_pages(pool: torch.Tensor, headroom: float = 1.5):
+    """An fp8 e4m3 copy of a 16-bit pool ([pages, Hkv, ...]) with one scale per
+    (page, kv head): amax x headroom / 448.  Returns (codes, scales float32)."""
+    p_, h_ = pool.shape[0], pool.shape[1]
+    amax = pool.float().abs().reshape(p_, h_, -1).amax(dim=2)
+    scales = torch.where(amax > 0, amax * headroom / 448.0, torch.ones_like(amax)).contiguous()
+    shape = (p_, h_) + (1,) * (pool.dim() - 2)
+    return (pool.float() / scales.view(shape)).clamp(-448, 448).to(torch.float8_e4m3fn), scales
+
+
+def to_fp8_k_layout(k_pool: torch.Tensor) -> torch.Tensor:
+    """16-bit K pool [P, H, HD/8, TPP, 8] -> the fp8 stripe layout's element
+    order [P, H, HD/16, TPP, 16] (same values)."""
+    p_, h_, c_, t_, x_ = k_pool.shape
+    tok = k_pool.permute(0, 1, 3, 2, 4).reshape(p_, h_, t_, c_ * x_)
+    return tok.reshape(p_, h_, t_, c_ * x_ // 16, 16).permute(0, 1, 3, 2, 4).contiguous()
+
+
 def traffic_bytes():
     """HBM bytes per decode call measured by the committed rocprofv3 counter
     passes (FETCH_SIZE scaled by 2, WRITE_SIZE by 1, calibrated on a 1 GiB
@@ -142,6 +160,26 @@ class DecodeWorkload:
     def decode(self, partition_size: int = 0):
         return pal.paged_attention_decode(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens,
                                           partition_size=partition_size)
+
+    def make_fp8(self):
+        """fp8 e4m3 pages of the same values (per-(page, kv head) scales), beside
+        the 16-bit pools."""
+        self.k8, self.ks = to_fp8_pages(to_fp8_k_layout(self.k_pool))
+        self.v8, self.vs = to_fp8_pages(self.v_pool)
+
+    def fill_fp8(self):
+        pal.fill_kv_pages(self.new_k, self.new_v, self.k8, self.v8, self.page_table, self.write_pos, self.q2seq,
+                          k_scales=self.ks, v_scales=self.vs)
+
+    def decode_fp8(self, partition_size: int = 0):
+        return pal.paged_attention_decode(self.queries, self.k8, self.v8, self.page_table, self.seq_lens,
+                                          partition_size=partition_size, k_scales=self.ks, v_scales=self.vs)
+
+    def decode_bytes_fp8(self) -> int:
+        """fp8 K/V bytes (1 per element) + their scales + Q and O."""
+        ctx = int(self.lens_np.astype(np.int64).sum())
+        pages = int(((self.lens_np.astype(np.int64) + self.tpp - 1) // self.tpp).sum())
+        return ctx * 2 * self.hkv * self.hd + pages * self.hkv * 2 * 4 + 2 * self.num_seqs * self.hq * self.hd * 2
 
     # algorithmic bytes (each byte the operation must move at least once)
     def decode_bytes(self) -> int:
@@ -248,6 +286,42 @@ class FusedWorkload:
     def attend(self):
         return pal.paged_attention(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens,
                                    self.q2seq, self.q_offset)
+
+
+class RopeFill:
+    """The fused RoPE + cast + scatter feeding a fill step: fp32 projection
+    rows (K, V and the queries) of the workload's new tokens, NeoX rotation
+    of K and Q over the whole head, cast to bf16, K/V scattered into the
+    workload's 16-bit pools."""
+
+    def __init__(self, w, device, seed: int = 9):
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        n = int(w.write_pos.numel())
+        self.n, self.hq, self.hkv, self.hd = n, w.hq, w.hkv, w.hd
+        self.k = torch.randn((n, w.hkv, w.hd), generator=g, device=device)
+        self.v = torch.randn((n, w.hkv, w.hd), generator=g, device=device)
+        self.q = torch.randn((n, w.hq, w.hd), generator=g, device=device)
+        self.pt, self.pos, self.q2s = w.page_table, w.write_pos, w.q2seq
+        self.k_pool, self.v_pool = w.k_pool, w.v_pool
+        self.table = pal.rope_cos_sin_cache(int(w.write_pos.max().item()) + 1, w.hd, 500000.0, device=device)
+
+    def run(self):
+        return pal.rope_fill_kv_pages(self.k, self.v, self.k_pool, self.v_pool, self.pt, self.pos, self.q2s,
+                                      self.table, queries=self.q)
+
+    def bytes(self) -> int:
+        """fp32 K, V, Q read + bf16 K, V, Q written + one cos/sin row per token."""
+        kv = 2 * self.n * self.hkv * self.hd
+        qn = self.n * self.hq * self.hd
+        return (kv + qn) * (4 + 2) + self.n * self.hd * 4
+
+    def report(self, ms: float) -> dict:
+        b = self.bytes()
+        return {"workload": f"rope_fill_kv_pages of {self.n} tokens: fp32 K/V/Q rows, NeoX RoPE, cast to bf16, "
+                            f"scatter (Hq {self.hq}, Hkv {self.hkv}, HD {self.hd})",
+                "ms": round(ms, 5), "bytes": b, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                "frac_of_hbm_peak": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 # ---------------------------------------------------------------------------
@@ -418,7 +492,34 @@ def main() -> int:
             "timing": "HIP events around back-to-back decode calls on the launch stream (stream + merge kernels)",
         },
     }
-    del works
+    # the same step over fp8 pages (bytes counted at one byte per K/V element)
+    # and the fused RoPE + cast + scatter feeding it (fp32 projection rows)
+    for w in works:
+        w.make_fp8()
+    rot = iter(range(1 << 30))
+    f8_dec_ms, _ = time_op(lambda: works[next(rot) % len(works)].decode_fp8(), args.steps, 3, stream)
+    rot = iter(range(1 << 30))
+
+    def fp8_step():
+        w = works[next(rot) % len(works)]
+        w.fill_fp8()
+        w.decode_fp8()
+
+    f8_step_ms, _ = time_op(fp8_step, args.steps, 3, stream)
+    f8_bytes = float(np.mean([w.decode_bytes_fp8() for w in works]))
+    rope = RopeFill(w0, dev)
+    rope_ms, _ = time_op(rope.run, args.steps, 3, stream)
+    result["fp8_pages"] = {
+        "workload": "config 2 over fp8 e4m3 pages (per-(page, kv head) scales), bf16 queries/output",
+        "decode_ms": round(f8_dec_ms, 5), "decode_bytes": int(f8_bytes),
+        "decode_GB/s": round(f8_bytes / (f8_dec_ms * 1e-3) / 1e9, 1),
+        "decode_frac_of_hbm_peak": round(f8_bytes / (f8_dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "speedup_vs_bf16_decode": round(dec_ms / f8_dec_ms, 3),
+        "step_ms (fill_fp8 + decode)": round(f8_step_ms, 5),
+        "tokens_per_s": round(w0.num_seqs / (f8_step_ms * 1e-3), 1),
+    }
+    result["rope_fill_config2"] = rope.report(rope_ms)
+    del works, rope
     torch.cuda.empty_cache()
     result.update(run_extra(configs, dev, args))
     if not args.no_cpu_baseline:
@@ -442,6 +543,12 @@ def run_extra(configs: set[str], dev, args) -> dict:
             gbs = nbytes / (ms * 1e-3) / 1e9
             res[f"partition_{part}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
                                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        w.make_fp8()
+        f8 = w.decode_bytes_fp8()
+        for part in (512, 0):
+            ms, _ = time_op(lambda: w.decode_fp8(part), steps, warm, stream)
+            res[f"fp8_partition_{part}"] = {"ms": round(ms, 4), "bytes": f8, "GB/s": round(f8 / (ms * 1e-3) / 1e9, 1),
+                                           "frac_of_hbm_peak": round(f8 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         out["long_context_decode"] = res
         del w
         torch.cuda.empty_cache()
@@ -460,6 +567,10 @@ def run_extra(configs: set[str], dev, args) -> dict:
             "fill_ms": round(fill_ms, 4), "fill_GB/s": round(w.fill_bytes() / (fill_ms * 1e-3) / 1e9, 1),
             "step_ms": round(att_ms + fill_ms, 4),
         }
+        rope = RopeFill(w, dev)
+        rope_ms, _ = time_op(rope.run, steps, warm, stream)
+        out["prefill"]["rope_fill"] = rope.report(rope_ms)
+        del rope
         del w
         torch.cuda.empty_cache()
     if "c5" in configs:

@@ -40,6 +40,17 @@ extern "C" {
 
 #define PAL_DTYPE_FLOAT16 0
 #define PAL_DTYPE_BFLOAT16 1
+/* fp8 e4m3 (OCP "fn": bias 7, max 448, no infinities) KV pages, each
+ * (page, kv head) block with an fp32 scale: value = fp8 * scale.  Pool
+ * layouts as above with x = 16 / sizeof(fp8) = 16.  The reference supports
+ * f16 / bf16 only (paged_attention_kernels.metal:41-42). */
+#define PAL_DTYPE_FP8_E4M3 2
+/* fp32 sources of the fused RoPE + cast + scatter (the projection output). */
+#define PAL_DTYPE_FLOAT32 3
+
+#define PAL_ROPE_NONE 0
+#define PAL_ROPE_NEOX 1 /* rotate halves: dims (f, f + rotary_dim / 2) */
+#define PAL_ROPE_GPTJ 2 /* rotate pairs: dims (2f, 2f + 1) */
 
 #define PAL_OK 0
 #define PAL_ERR_INVALID_ARGUMENT (-1)
@@ -85,6 +96,48 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
                       int64_t num_seqs, int64_t page_table_width, void* stream);
 
 /*
+ * fill_kv_pages into fp8 e4m3 pools (no reference counterpart: the
+ * reference's pools are f16 / bf16 only; this extends ops.py:133-171 with the
+ * same index math, fill_kv_pages.h.metal:65-116, and x = 16 for the K stripe,
+ * paged_attention_decode_primitive.cpp:384-397).  new_keys / new_values
+ * ([N, Hkv, HD], src_dtype f16, bf16 or f32) are quantized with the
+ * caller's per-(page, kv head) scales (k_scales / v_scales, fp32
+ * [num_pages, Hkv]): q = x / scale, held to [-448, 448], rounded to nearest
+ * even.  head_dim % 16 == 0, head_dim <= 256.  In place.
+ */
+int pal_fill_kv_pages_fp8(const void* new_keys, const void* new_values, int src_dtype, void* k_pool, void* v_pool,
+                          const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                          const int32_t* write_positions, const uint32_t* query_to_seq_map, int64_t num_tokens,
+                          int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages, int64_t num_seqs,
+                          int64_t page_table_width, void* stream);
+
+/*
+ * RoPE + cast + scatter in one pass: the step that produces fill_kv_pages'
+ * inputs (ops.py:133-171 -> fill_kv_pages.h.metal:56-116) fused with it.
+ * No reference counterpart.  For token t at position p = write_positions[t]:
+ * K (and, when queries is given, every query head of the token) is rotated
+ * by the angles of row p of cos_sin_cache ([cos_sin_rows, rotary_dim] fp32:
+ * cos of the rotary_dim / 2 frequencies, then their sin): NeoX style
+ * (PAL_ROPE_NEOX) pairs dims (f, f + rotary_dim / 2), GPT-J style
+ * (PAL_ROPE_GPTJ) pairs (2f, 2f + 1); dims at and past rotary_dim pass
+ * through.  x' = x cos - y sin, y' = y cos + x sin in fp32, each product
+ * rounded (no fused multiply-add).  K and V are then cast to kv_dtype
+ * (f16 / bf16: round to nearest even; fp8: as pal_fill_kv_pages_fp8) and
+ * scattered as fill_kv_pages does; the rotated queries are cast to
+ * q_out_dtype (f16 / bf16) into queries_out ([N, Hq, HD]).  Tokens whose
+ * position has no row in the table are not written to the pools; their
+ * queries are cast without rotation.  head_dim <= 256; NeoX needs
+ * rotary_dim % 16 == 0, GPT-J rotary_dim % 8 == 0.
+ */
+int pal_rope_fill_kv_pages(const void* new_keys, const void* new_values, int src_dtype, void* k_pool, void* v_pool,
+                           int kv_dtype, const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                           const int32_t* write_positions, const uint32_t* query_to_seq_map, int64_t num_tokens,
+                           int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages, int64_t num_seqs,
+                           int64_t page_table_width, const float* cos_sin_cache, int64_t cos_sin_rows,
+                           int rotary_dim, int rope_style, const void* queries, void* queries_out,
+                           int num_q_heads, int q_out_dtype, void* stream);
+
+/*
  * Workspace bytes pal_paged_attention_decode needs for these shapes on the
  * current device (0 for unsupported arguments or when no device is present).
  * The workspace holds a scan of the sequence lengths, a work-claim counter
@@ -127,6 +180,25 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                int tokens_per_page, int64_t num_pages, int64_t page_table_width,
                                int partition_size, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/*
+ * paged_attention_decode over fp8 e4m3 pools (no reference counterpart: the
+ * reference's pools are f16 / bf16, paged_attention_kernels.metal:41-42; the
+ * semantics are those of pal_paged_attention_decode, ops.py:42-84).  Keys
+ * and values are the pools' codes times their (page, kv head) scale
+ * (k_scales / v_scales, fp32 [num_pages, Hkv]); queries, output and the
+ * arithmetic stay in dtype (f16 / bf16).  head_dim 64, 128 or 256.  The
+ * workspace size comes from pal_paged_attention_decode_fp8_workspace_size.
+ */
+size_t pal_paged_attention_decode_fp8_workspace_size(int dtype, int64_t num_seqs, int num_q_heads, int num_kv_heads,
+                                                     int head_dim, int tokens_per_page, int64_t page_table_width,
+                                                     int partition_size);
+int pal_paged_attention_decode_fp8(const void* queries, const void* k_pool, const void* v_pool,
+                                   const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                                   const int32_t* sequence_lengths, void* out, int dtype, int64_t num_query_rows,
+                                   int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                   int tokens_per_page, int64_t num_pages, int64_t page_table_width,
+                                   int partition_size, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * No counterpart in the reference.  The same operation as

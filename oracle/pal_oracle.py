@@ -24,6 +24,14 @@ It restates, in numpy, what the reference computes on the hot path:
 * ``paged_attention`` (fused mixed batch) has no reference function; its
   semantics are defined by this build: row r of sequence s = q2seq[r] attends
   to the keys [0, min(seq_lens[s], q_offset[r])) of s, all read from pages.
+* ``fp8_e4m3_encode`` / ``fp8_e4m3_decode`` / ``quantize_fp8`` -- fp8 KV
+  pages (no reference counterpart: the reference stores f16 / bf16 only,
+  paged_attention_kernels.metal:41-42); OCP e4m3 "fn" (bias 7, 3 mantissa
+  bits, max 448, no infinities), round to nearest even.
+* ``rope_cos_sin_cache`` / ``apply_rope`` / ``fill_kv_pages_ex`` -- the step
+  feeding fill_kv_pages (RoPE of K and Q, cast to the pool dtype) fused with
+  its scatter; the scatter is that of fill_kv_pages.h.metal:65-116 with the
+  K stripe x = 16 / sizeof(T) (paged_attention_decode_primitive.cpp:384-397).
 
 All pools and activations are handled as raw 16-bit patterns (uint16) plus a
 dtype tag ("f16" or "bf16"), so bf16 needs no numpy dtype and fill parity can
@@ -40,7 +48,14 @@ Pinning (what checks this oracle, in tests/test_oracle.py):
     decode/test_softmax_and_value.py, prefill/test_softmax_and_value.py,
     invariance under page-table permutation, and a brute-force scalar loop
     on tiny shapes;
-  * two-pass: equality with the single-pass result (any chunk size).
+  * two-pass: equality with the single-pass result (any chunk size);
+  * fp8 encode / decode: torch.float8_e4m3fn on every finite value, on the
+    midpoints between neighbours (ties to even) and on random values;
+  * RoPE: position 0 is the identity, rotations preserve the norm of every
+    rotated pair, rotating by p then q equals rotating by p + q (to fp32
+    rounding), GPT-J and NeoX styles agree after the matching permutation of
+    dims, and a torch fp32 restatement (same operation order) agrees bit for
+    bit; the cos/sin table matches its closed form (row 0 = (1, 0)).
 The reference's epsilon (+1e-6 in denominators) and -88 exp clamp are not
 reproduced: their relative effect is below 1e-6.
 """
@@ -84,11 +99,78 @@ def f32_to_bits(x: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(f"unsupported dtype {dtype!r}")
 
 
+FP8_MAX = 448.0
+
+
+def fp8_e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """uint8 e4m3 codes -> float32.  Exponent field e (4 bits, bias 7),
+    mantissa m (3 bits): e == 0 -> m * 2^-9 (subnormal); e == 15 and m == 7 ->
+    NaN (the only non-finite codes, sign either way); else (1 + m/8) 2^(e-7)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int32)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e.astype(np.float64) - 7.0))
+    out = (sign * mag).astype(np.float32)
+    out[(e == 15) & (m == 7)] = np.nan
+    return out
+
+
+def fp8_e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """float32 -> uint8 e4m3 code, round to nearest even, for |x| <= 448
+    (larger magnitudes and NaN give the NaN code 0x7F / 0xFF; callers clamp
+    first).  Works on the exact binary value: |x| = f * 2^k with f in [1, 2)
+    (frexp), mantissa (f - 1) * 8 rounded half to even; below 2^-6 the value
+    is a multiple of 2^-9 rounded half to even."""
+    x = np.asarray(x, dtype=np.float32).astype(np.float64)
+    neg = np.signbit(x)
+    a = np.abs(x)
+    sub = a < 2.0 ** -6
+    # subnormal range: a multiple of 2^-9 (an exact scaling; rint rounds half
+    # to even); 8 becomes 0b0001000, the smallest normal
+    n_sub = np.rint(np.where(sub, a, 0.0) * 2.0 ** 9).astype(np.int64)
+    fr, ex = np.frexp(np.where(sub | ~np.isfinite(a), 1.0, a))  # a = fr * 2^ex, fr in [0.5, 1)
+    k = ex.astype(np.int64) - 1  # a = (2 fr) 2^k
+    mant = np.rint((2.0 * fr - 1.0) * 8.0).astype(np.int64)
+    k = np.where(mant == 8, k + 1, k)
+    mant = np.where(mant == 8, 0, mant)
+    normal = ((k + 7) << 3) | mant
+    code = np.where(sub, n_sub, normal)
+    bad = ~np.isfinite(a) | (a > FP8_MAX) | (~sub & (code > 0x7E))
+    code = np.where(bad, 0x7F, code)
+    code = code | np.where(neg, 0x80, 0)
+    return code.astype(np.uint8)
+
+
+def quantize_fp8(x: np.ndarray, scale) -> np.ndarray:
+    """The fill's fp8 quantization: q = x / scale in float32 (correctly
+    rounded), held to [-448, 448] with NaN kept, then e4m3 round to nearest
+    even."""
+    q = np.asarray(x, np.float32) / np.asarray(scale, np.float32)
+    q = np.where(q > FP8_MAX, np.float32(FP8_MAX), q)
+    q = np.where(q < -FP8_MAX, np.float32(-FP8_MAX), q)
+    return fp8_e4m3_encode(q.astype(np.float32))
+
+
+def pool_to_f32(pool: np.ndarray, kv_dtype: str, scales=None) -> np.ndarray:
+    """A K or V pool as float32 values: 16-bit bits decoded, or fp8 codes
+    decoded and multiplied by their (page, kv head) scale ([P, Hkv])."""
+    if kv_dtype in ("f16", "bf16"):
+        return bits_to_f32(pool, kv_dtype)
+    if kv_dtype != "fp8":
+        raise ValueError(f"unsupported pool dtype {kv_dtype!r}")
+    vals = fp8_e4m3_decode(pool)
+    sc = np.asarray(scales, np.float32).reshape(pool.shape[:2] + (1,) * (pool.ndim - 2))
+    return (vals * sc).astype(np.float32)
+
+
 def stripe_size(dtype: str) -> int:
     """K-cache stripe width x = 16 / sizeof(T) (bindings.cpp:44-48)."""
-    if dtype not in ("f16", "bf16"):
-        raise ValueError(f"unsupported dtype {dtype!r}")
-    return MEMORY_ALIGNMENT_BYTES // 2
+    if dtype in ("f16", "bf16"):
+        return MEMORY_ALIGNMENT_BYTES // 2
+    if dtype == "fp8":
+        return MEMORY_ALIGNMENT_BYTES
+    raise ValueError(f"unsupported dtype {dtype!r}")
 
 
 # ---------------------------------------------------------------------------
@@ -126,6 +208,117 @@ def fill_kv_pages(new_k, new_v, k_pool, v_pool, page_table, write_pos, q2seq):
         k_out[page[t], :, :, slot[t], :] = nk[t]
         v_out[page[t], :, :, slot[t]] = nv[t]
     return k_out, v_out
+
+
+# ---------------------------------------------------------------------------
+# RoPE + cast + scatter (the step feeding fill_kv_pages, fused with it)
+# ---------------------------------------------------------------------------
+
+
+def rope_cos_sin_cache(max_position: int, rotary_dim: int, base: float = 10000.0) -> np.ndarray:
+    """[max_position, rotary_dim] float32: cos(p w_f) for f < rotary_dim / 2,
+    then sin(p w_f), with w_f = base^(-2f / rotary_dim), computed in float64
+    and rounded once."""
+    half = rotary_dim // 2
+    inv_freq = base ** (-(2.0 * np.arange(half, dtype=np.float64)) / rotary_dim)
+    ang = np.arange(max_position, dtype=np.float64)[:, None] * inv_freq[None, :]
+    return np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+
+
+def apply_rope(x: np.ndarray, positions, table: np.ndarray, rotary_dim: int, style: str) -> np.ndarray:
+    """Rotate [N, H, HD] float32 rows by the angles of their positions.
+
+    style "neox": dims (f, f + rot/2) form pair f; "gptj": dims (2f, 2f+1).
+    x' = x cos - y sin, y' = y cos + x sin, each product and sum rounded to
+    float32 separately (no fused multiply-add).  Dims >= rotary_dim pass
+    through; rows whose position is outside the table pass through
+    unrotated."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    pos = np.asarray(positions, np.int64)
+    half = rotary_dim // 2
+    ok = (pos >= 0) & (pos < table.shape[0])
+    rows = table[np.where(ok, pos, 0)]
+    c = rows[:, None, :half]
+    s_ = rows[:, None, half:rotary_dim]
+    if style == "neox":
+        a = x[:, :, :half].copy()
+        b = x[:, :, half:rotary_dim].copy()
+    elif style == "gptj":
+        a = x[:, :, 0:rotary_dim:2].copy()
+        b = x[:, :, 1:rotary_dim:2].copy()
+    else:
+        raise ValueError(f"unknown rope style {style!r}")
+    na = (a * c).astype(np.float32) - (b * s_).astype(np.float32)
+    nb = (b * c).astype(np.float32) + (a * s_).astype(np.float32)
+    na = np.where(ok[:, None, None], na, a)
+    nb = np.where(ok[:, None, None], nb, b)
+    if style == "neox":
+        x[:, :, :half] = na
+        x[:, :, half:rotary_dim] = nb
+    else:
+        x[:, :, 0:rotary_dim:2] = na
+        x[:, :, 1:rotary_dim:2] = nb
+    return x
+
+
+def cast_to_pool(x: np.ndarray, kv_dtype: str, scales=None) -> np.ndarray:
+    """float32 values -> pool element codes: f16 / bf16 bits (round to nearest
+    even), or fp8 codes quantized with one scale per row ([N, Hkv] scales
+    broadcast over the last dim)."""
+    if kv_dtype in ("f16", "bf16"):
+        return f32_to_bits(x, kv_dtype)
+    return quantize_fp8(x, np.asarray(scales, np.float32)[..., None])
+
+
+def fill_kv_pages_ex(new_k, new_v, k_pool, v_pool, kv_dtype, page_table, write_pos, q2seq, *,
+                     k_scales=None, v_scales=None, rope=None, queries=None, q_out_dtype=None):
+    """fill_kv_pages generalised: float32 source rows (the projection output),
+    optional RoPE of K (and Q), cast to the pool dtype, scatter.
+
+    new_k / new_v: [N, Hkv, HD] float32 values.  Pools: element codes (uint16
+    bits for f16 / bf16, uint8 fp8 codes), K [P, Hkv, HD/x, TPP, x] with
+    x = stripe_size(kv_dtype).  fp8: k_scales / v_scales [P, Hkv]; the value
+    stored is quantize_fp8(x, scale of the destination (page, head)).  rope:
+    None or (table, rotary_dim, style); the position is write_pos.  Tokens
+    with no valid destination (sequence, position, page out of range, or a
+    position outside the table) are skipped, as the kernel does.  Returns
+    (k_out, v_out, q_out): copies of the pools, and the rotated queries'
+    bits in q_out_dtype (None without queries).  Index math of
+    fill_kv_pages.h.metal:65-116.
+    """
+    k_out = np.array(k_pool, copy=True)
+    v_out = np.array(v_pool, copy=True)
+    n = int(new_k.shape[0])
+    _, hkv, nstripe, tpp, x = k_out.shape
+    hd = nstripe * x
+    kf = np.asarray(new_k, np.float32)
+    vf = np.asarray(new_v, np.float32)
+    pos = np.asarray(write_pos, np.int64)
+    q_out = None
+    if rope is not None:
+        table, rot, style = rope
+        kf = apply_rope(kf, pos, table, rot, style)
+        if queries is not None:
+            q_out = f32_to_bits(apply_rope(np.asarray(queries, np.float32), pos, table, rot, style), q_out_dtype)
+    pt = np.asarray(page_table).astype(np.int64)
+    seq = np.asarray(q2seq).astype(np.int64)
+    for t in range(n):
+        s_, p_ = int(seq[t]), int(pos[t])
+        if s_ >= pt.shape[0] or p_ < 0 or p_ // tpp >= pt.shape[1]:
+            continue
+        if rope is not None and p_ >= rope[0].shape[0]:
+            continue
+        page = int(pt[s_, p_ // tpp])
+        if page >= k_out.shape[0]:
+            continue
+        slot = p_ % tpp
+        ks = None if k_scales is None else np.asarray(k_scales)[page]
+        vs = None if v_scales is None else np.asarray(v_scales)[page]
+        kc = cast_to_pool(kf[t], kv_dtype, ks)  # [Hkv, HD]
+        vc = cast_to_pool(vf[t], kv_dtype, vs)
+        k_out[page, :, :, slot, :] = kc.reshape(hkv, nstripe, x)
+        v_out[page, :, :, slot] = vc.reshape(hkv, hd)
+    return k_out, v_out, q_out
 
 
 # ---------------------------------------------------------------------------
@@ -188,8 +381,12 @@ def attend(q, k, v, limits, causal_pos=None):
     return out
 
 
-def _pools_f32(k_pool, v_pool, dtype):
-    return bits_to_f32(k_pool, dtype), bits_to_f32(v_pool, dtype)
+def _pools_f32(k_pool, v_pool, dtype, kv=None):
+    """float32 pools: kv = None means 16-bit pools of the query dtype; else
+    kv = (k_scales, v_scales) of fp8 pools."""
+    if kv is None:
+        return bits_to_f32(k_pool, dtype), bits_to_f32(v_pool, dtype)
+    return pool_to_f32(k_pool, "fp8", kv[0]), pool_to_f32(v_pool, "fp8", kv[1])
 
 
 # ---------------------------------------------------------------------------
@@ -197,17 +394,19 @@ def _pools_f32(k_pool, v_pool, dtype):
 # ---------------------------------------------------------------------------
 
 
-def paged_attention_decode(queries, k_pool, v_pool, page_table, seq_lens, dtype):
+def paged_attention_decode(queries, k_pool, v_pool, page_table, seq_lens, dtype, kv_scales=None):
     """Decode: one query row per sequence over its paged context.
 
     queries: [N, Hq, HD] (or [N, HD] meaning Hq = 1) uint16 bits, N >= S; row s
     serves sequence s and rows >= S are ignored (decode.h.metal:106-108).
-    Returns [S, Hq, HD] float32 (decode_primitive.cpp:289-300).
+    kv_scales: None for 16-bit pools of the query dtype, or (k_scales,
+    v_scales) of fp8 pools.  Returns [S, Hq, HD] float32
+    (decode_primitive.cpp:289-300).
     """
     q = bits_to_f32(queries, dtype)
     if q.ndim == 2:
         q = q[:, None, :]
-    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    kf, vf = _pools_f32(k_pool, v_pool, dtype, kv_scales)
     s_count = int(np.asarray(page_table).shape[0])
     hq, hd = q.shape[1], q.shape[2]
     out = np.zeros((s_count, hq, hd), np.float32)
@@ -266,7 +465,7 @@ def paged_attention_decode_two_pass(queries, k_pool, v_pool, page_table, seq_len
 
 
 def paged_attention_prefill(q_prompt, k_prompt, v_prompt, k_pool, v_pool, page_table,
-                            context_lens, dtype):
+                            context_lens, dtype, kv_scales=None):
     """Prefill over paged history plus a causal dense prompt.
 
     q_prompt: [S*P, Hq, HD]; k_prompt/v_prompt: [S*P, Hkv, HD]; P is uniform,
@@ -279,7 +478,7 @@ def paged_attention_prefill(q_prompt, k_prompt, v_prompt, k_pool, v_pool, page_t
     q = bits_to_f32(q_prompt, dtype)
     kp = bits_to_f32(k_prompt, dtype)
     vp = bits_to_f32(v_prompt, dtype)
-    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    kf, vf = _pools_f32(k_pool, v_pool, dtype, kv_scales)
     pt = np.asarray(page_table)
     s_count = int(pt.shape[0])
     rows, hq, hd = q.shape
@@ -297,7 +496,7 @@ def paged_attention_prefill(q_prompt, k_prompt, v_prompt, k_pool, v_pool, page_t
     return out.reshape(rows * hq, hd)
 
 
-def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offset, dtype):
+def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offset, dtype, kv_scales=None):
     """Fused mixed batch (build-defined; no reference function exists).
 
     Row r belongs to sequence s = q2seq[r] and attends to the keys
@@ -307,7 +506,7 @@ def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offs
     sequence, are zero.  Returns [R, Hq, HD] float32.
     """
     q = bits_to_f32(queries, dtype)
-    kf, vf = _pools_f32(k_pool, v_pool, dtype)
+    kf, vf = _pools_f32(k_pool, v_pool, dtype, kv_scales)
     pt = np.asarray(page_table)
     lens = np.asarray(seq_lens).astype(np.int64)
     seqs = np.asarray(q2seq).astype(np.int64)

@@ -233,7 +233,7 @@ struct ItemLds {
 // between virtual workers: while the last blocks of a piece are computed,
 // the first blocks of the next piece are already loading (its item, query
 // and first page ids were fetched when the piece before it started).
-template <int DT, int HD, int TPP, int PF, bool kMultiV>
+template <int DT, int HD, int TPP, int PF, bool kMultiV, bool KV8>
 __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched& sc, const int64_t* cum,
                                               const ItemLds il, int64_t n_items, int64_t v_begin,
                                               int64_t v_end) {
@@ -241,6 +241,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   constexpr int KK = kK32 ? HD / 32 : HD / 16;
   constexpr int NT = HD / 16;            // output tiles of 16 dims
   constexpr int NBUF = PF + 1;
+  // fp8 pools: a K stripe is 16 dims of one token (16 bytes); lane group g
+  // loads stripes g + 4j, j < KL8, each feeding two k-steps of 8 dims
+  constexpr int EB = KV8 ? 1 : 2;        // pool element bytes
+  constexpr int KL8 = HD / 64;
+  static_assert(!KV8 || (HD % 64 == 0), "fp8 pools: head_dim a multiple of 64");
 
   const int64_t b0 = vstart(sc, v_begin);
   const int64_t b_end = vstart(sc, v_end);
@@ -266,7 +271,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   const int g = lane >> 4;
   const int r16 = lane & 15;
   const int segs = p.num_kv_heads * p.head_chunks;
-  const int64_t head_block = static_cast<int64_t>(HD) * TPP;  // elements per (page, kv head)
+  const int64_t head_block = static_cast<int64_t>(HD) * TPP * EB;  // bytes per (page, kv head)
   const int64_t page_stride = head_block * p.num_kv_heads;
 
   // A piece: item s (query row s of page-table row `seq`, `len` keys, nb
@@ -321,7 +326,9 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     const uint16_t* qrow = p.q + (s * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      if constexpr (kK32) {
+      if constexpr (KV8) {  // k-step kk = (stripe j = kk / 2, half): dims 16 (g + 4j) + 8 half .. +7
+        q4[kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * (g + 4 * (kk >> 1)) + 8 * (kk & 1)) & qmask;
+      } else if constexpr (kK32) {
         q4[kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * g) & qmask;
       } else {
         q2[kk] = *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 4 * g) & qmask;
@@ -356,9 +363,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   uint32_t pid_cur = load_window(c_seq, c_blk, 0), pid_nxt = load_window(c_seq, c_blk, 1),
            pid_later = load_window(c_seq, c_blk, 2);
 
-  u32x4 kb4[NBUF][kK32 ? KK : 1];
+  u32x4 kb4[NBUF][KV8 ? KL8 : (kK32 ? KK : 1)];
   u32x2 kb2[NBUF][kK32 ? 1 : KK];
-  u32x2 vb[NBUF][NT];
+  u32x2 vb[NBUF][KV8 ? 1 : NT];
+  uint32_t vb8[NBUF][KV8 ? NT : 1];
+  float bks[NBUF], bvs[NBUF];  // fp8: the block's (page, kv head) scales
   bool bv[NBUF];
 
   bool first = true;     // the piece is its virtual worker's first
@@ -379,10 +388,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     const int64_t n_pad = (n_blk + NBUF - 1) / NBUF * NBUF;  // steps of the piece
     const int64_t bstart = c_blk;                          // first block of the piece
     const int64_t pbase = (bstart * 16) / TPP;               // its page index
-    const uint16_t* kbase = p.k_pool + kvh * head_block;
-    const uint16_t* vbase = p.v_pool + kvh * head_block;
-    const uint16_t* kbase_n = kbase;  // set once the next piece is known
-    const uint16_t* vbase_n = vbase;
+    const uint8_t* kbase = static_cast<const uint8_t*>(p.k_pool) + kvh * head_block;
+    const uint8_t* vbase = static_cast<const uint8_t*>(p.v_pool) + kvh * head_block;
+    const uint8_t* kbase_n = kbase;  // set once the next piece is known
+    const uint8_t* vbase_n = vbase;
+    int kvh_n = kvh;
     int64_t nblk_n = 1;
     int64_t bstart_n = 0, pbase_n = 0;  // first block of the next piece and its page index
 
@@ -408,24 +418,40 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       bv[buf] = pg < p.num_pages;
       const uint32_t page = bv[buf] ? pg : 0u;
       const int slot0 = static_cast<int>((b * 16) % TPP);
-      const uint16_t* kb_x = kbase_n;
-      const uint16_t* vb_x = vbase_n;
-      const uint16_t* kp = (to_next ? kb_x : kbase) + static_cast<int64_t>(page) * page_stride;
-      const uint16_t* vp = (to_next ? vb_x : vbase) + static_cast<int64_t>(page) * page_stride + slot0 + 4 * g;
+      const uint8_t* kb_x = kbase_n;
+      const uint8_t* vb_x = vbase_n;
+      const uint8_t* kp = (to_next ? kb_x : kbase) + static_cast<int64_t>(page) * page_stride;
+      const uint8_t* vp = (to_next ? vb_x : vbase) + static_cast<int64_t>(page) * page_stride + (slot0 + 4 * g) * EB;
+      if constexpr (KV8) {
+        const int kvh_b = to_next ? kvh_n : kvh;
+        const int64_t si = static_cast<int64_t>(page) * p.num_kv_heads + kvh_b;
+        bks[buf] = p.k_scales[si];
+        bvs[buf] = p.v_scales[si];
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        if constexpr (kK32) {
-          const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
-          kb4[buf][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 8));
-        } else {
-          const int d = 16 * kk + 4 * g;  // dims d .. d+3
-          kb2[buf][kk] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x2*>(kp + ((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7)));
+        for (int j = 0; j < KL8; ++j) {
+          const int c = g + 4 * j;  // stripe of dims 16c .. 16c+15
+          kb4[buf][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
         }
-      }
 #pragma unroll
-      for (int n = 0; n < NT; ++n)
-        vb[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP));
+        for (int n = 0; n < NT; ++n)
+          vb8[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vp + (16 * n + r16) * TPP));
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          if constexpr (kK32) {
+            const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
+            kb4[buf][kk] =
+                __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
+          } else {
+            const int d = 16 * kk + 4 * g;  // dims d .. d+3
+            kb2[buf][kk] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x2*>(kp + (((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7)) * 2));
+          }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          vb[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP * 2));
+      }
     };
 
     float m_run = -INFINITY;  // running max (raw score units) of head r16
@@ -438,12 +464,27 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       const int64_t b = bstart + i;
       const bool live = bv[buf] && i < n_blk;  // steps past the piece end are fully masked
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KV8) {
+        // 16 fp8 values (one stripe) -> two 8-element operands, exactly
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        if constexpr (kK32) {
-          acc = Dt<DT>::mma16x16x32(kb4[buf][kk], qv4[kk], acc);
-        } else {
-          acc = Dt<DT>::mma16x16x16(kb2[buf][kk], qv2[kk], acc);
+        for (int j = 0; j < KL8; ++j) {
+          const u32x4 w = kb4[buf][j];
+          const u32x4 lo = {Dt<DT>::fp8x2(w.x, false), Dt<DT>::fp8x2(w.x, true), Dt<DT>::fp8x2(w.y, false),
+                            Dt<DT>::fp8x2(w.y, true)};
+          const u32x4 hi = {Dt<DT>::fp8x2(w.z, false), Dt<DT>::fp8x2(w.z, true), Dt<DT>::fp8x2(w.w, false),
+                            Dt<DT>::fp8x2(w.w, true)};
+          acc = Dt<DT>::mma16x16x32(lo, qv4[2 * j], acc);
+          acc = Dt<DT>::mma16x16x32(hi, qv4[2 * j + 1], acc);
+        }
+        acc *= bks[buf];  // the block's K scale
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          if constexpr (kK32) {
+            acc = Dt<DT>::mma16x16x32(kb4[buf][kk], qv4[kk], acc);
+          } else {
+            acc = Dt<DT>::mma16x16x16(kb2[buf][kk], qv2[kk], acc);
+          }
         }
       }
       // tokens past the end (and whole invalid blocks) are masked
@@ -473,14 +514,22 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
         pe[e] = __builtin_amdgcn_exp2f(fmaf(sc4[e], p.scale_log2, -msc));
         l_run += pe[e];
       }
-      const u32x2 pb = {Dt<DT>::pack2(pe[0], pe[1]), Dt<DT>::pack2(pe[2], pe[3])};
+      // fp8: the block's V scale rides on the probabilities (the exp-sum stays unscaled)
+      const float pvs = KV8 ? bvs[buf] : 1.f;
+      const u32x2 pb = {Dt<DT>::pack2(pe[0] * pvs, pe[1] * pvs), Dt<DT>::pack2(pe[2] * pvs, pe[3] * pvs)};
       // slots past the end may hold anything, NaN bits included: zero their
       // V (branch-free: two ANDs per tile)
       const uint32_t mlo = (t0 < len ? 0x0000FFFFu : 0u) | (t0 + 1 < len ? 0xFFFF0000u : 0u);
       const uint32_t mhi = (t0 + 2 < len ? 0x0000FFFFu : 0u) | (t0 + 3 < len ? 0xFFFF0000u : 0u);
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const u32x2 vv = {vb[buf][n].x & mlo, vb[buf][n].y & mhi};
+        u32x2 vr;
+        if constexpr (KV8) {
+          vr = u32x2{Dt<DT>::fp8x2(vb8[buf][n], false), Dt<DT>::fp8x2(vb8[buf][n], true)};
+        } else {
+          vr = vb[buf][n];
+        }
+        const u32x2 vv = {vr.x & mlo, vr.y & mhi};
         o[n] = Dt<DT>::mma16x16x16(vv, pb, o[n]);
       }
     };
@@ -523,8 +572,9 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     const uint32_t pidn1 = load_window(x_seq, x_blk, 1);
     {
       const int kvh_x = x_seg / p.head_chunks;
-      kbase_n = p.k_pool + kvh_x * head_block;
-      vbase_n = p.v_pool + kvh_x * head_block;
+      kbase_n = static_cast<const uint8_t*>(p.k_pool) + kvh_x * head_block;
+      vbase_n = static_cast<const uint8_t*>(p.v_pool) + kvh_x * head_block;
+      kvh_n = kvh_x;
       nblk_n = x_count;
       bstart_n = x_blk;
       pbase_n = (x_blk * 16) / TPP;
@@ -636,7 +686,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #undef PAL_FIND_PIECE
 }
 
-template <int DT, int HD, int TPP, int PF, bool kChunks>
+template <int DT, int HD, int TPP, int PF, bool kChunks, bool KV8>
 __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_lds, int64_t* len_lds,
                                             int32_t* seq_lds, int64_t* wave_sums) {
   const bool lds_plan = p.num_seqs <= kInlinePlanSeqs;
@@ -694,16 +744,16 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
     // still its own virtual worker (its own partials and merge-list slot)
     const int64_t nw = p.num_workers;
     const int64_t va = w * sc.nc / nw, vb = (w + 1) * sc.nc / nw;
-    if (va < vb) process_range<DT, HD, TPP, PF, true>(p, sc, cum, il, n_items, va, vb);
+    if (va < vb) process_range<DT, HD, TPP, PF, true, KV8>(p, sc, cum, il, n_items, va, vb);
   } else {
-    if (w < sc.nws) process_range<DT, HD, TPP, PF, false>(p, sc, cum, il, n_items, w, w + 1);
+    if (w < sc.nws) process_range<DT, HD, TPP, PF, false, KV8>(p, sc, cum, il, n_items, w, w + 1);
     if constexpr (kStaticShareNum < kStaticShareDen) {  // a dynamically claimed tail is compiled in
       while (sc.nc > 0) {
         uint32_t k = 0;
         if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
         k = __builtin_amdgcn_readfirstlane(k);
         if (k >= sc.nc) break;
-        process_range<DT, HD, TPP, PF, false>(p, sc, cum, il, n_items, sc.nws + k, sc.nws + k + 1);
+        process_range<DT, HD, TPP, PF, false, KV8>(p, sc, cum, il, n_items, sc.nws + k, sc.nws + k + 1);
       }
     }
   }
@@ -714,7 +764,7 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
 // SIMD, measured slower.)  kChunks: the fixed-chunk mode (partition_size >
 // 0), a separate instantiation so the equal-share kernel keeps its lower
 // register count.
-template <int DT, int HD, int TPP, bool kChunks>
+template <int DT, int HD, int TPP, bool kChunks, bool KV8>
 __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const DecodeParams p) {
   __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
   __shared__ int64_t len_lds[kInlinePlanSeqs];
@@ -723,8 +773,10 @@ __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const Deco
   // Fixed chunks are 8, 16 or 32 blocks: three blocks of prefetch make the
   // steps of a chunk a whole number of step groups (no padded step per
   // chunk; measured 2 % faster in the 512-token mode of config 3).
-  constexpr int kPf = kChunks && HD <= 128 ? kPrefetch + 1 : kPrefetch;  // (head_dim 256 would spill)
-  stream_body<DT, HD, TPP, kPf, kChunks>(p, cum_lds, len_lds, seq_lds, wave_sums);
+  // fp8 pools: a block is half the bytes and registers, so one more block
+  // in flight keeps the bytes in flight per wavefront up
+  constexpr int kPf = KV8 ? kPrefetch + 1 : (kChunks && HD <= 128 ? kPrefetch + 1 : kPrefetch);  // (bf16 head_dim 256 would spill)
+  stream_body<DT, HD, TPP, kPf, kChunks, KV8>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Decode rows of the fused op: one workgroup per CU, held to half of the
@@ -741,14 +793,14 @@ constexpr int shared_cu_prefetch() {
   return HD == 128 ? kPrefetch - 1 : kPrefetch;
 }
 
-template <int DT, int HD, int TPP>
+template <int DT, int HD, int TPP, bool KV8>
 __global__ __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_shared_cu_kernel(const DecodeParams p) {
   __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
   __shared__ int64_t len_lds[kInlinePlanSeqs];
   __shared__ int32_t seq_lds[kInlinePlanSeqs];
   __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), false>(p, cum_lds, len_lds, seq_lds, wave_sums);
+  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), false, KV8>(p, cum_lds, len_lds, seq_lds, wave_sums);
 }
 
 // Walks the merge list, slot v for virtual worker v (first block < 0:
@@ -941,7 +993,7 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
   }
 }
 
-template <int DT, int HD, int TPP>
+template <int DT, int HD, int TPP, bool KV8>
 hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t stream) {
   hipError_t err;
   if (p.num_seqs > kInlinePlanSeqs) {
@@ -953,16 +1005,16 @@ hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t st
   bool plain = true;
   if constexpr (shares_cu(HD)) {
     if (shared_cu) {
-      hipLaunchKernelGGL((decode_shared_cu_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(groups)),
+      hipLaunchKernelGGL((decode_shared_cu_kernel<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(groups)),
                          dim3(kGroupThreads), 0, stream, p);
       plain = false;
     }
   }
   if (plain && p.tokens_per_worker > 0)
-    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, true>), dim3(static_cast<unsigned>(groups)),
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, true, KV8>), dim3(static_cast<unsigned>(groups)),
                        dim3(kGroupThreads), 0, stream, p);
   else if (plain)
-    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, false>), dim3(static_cast<unsigned>(groups)),
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, false, KV8>), dim3(static_cast<unsigned>(groups)),
                        dim3(kGroupThreads), 0, stream, p);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -978,44 +1030,64 @@ hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t st
   return hipGetLastError();
 }
 
-template <int DT, int HD>
+template <int DT, int HD, bool KV8>
 hipError_t dispatch_tpp(const DecodeParams& p, int tpp, bool shared_cu, hipStream_t stream) {
   switch (tpp) {
-    case 16: return launch_decode_t<DT, HD, 16>(p, shared_cu, stream);
-    case 32: return launch_decode_t<DT, HD, 32>(p, shared_cu, stream);
+    case 16: return launch_decode_t<DT, HD, 16, KV8>(p, shared_cu, stream);
+    case 32: return launch_decode_t<DT, HD, 32, KV8>(p, shared_cu, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int DT>
-hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, bool shared_cu, hipStream_t stream) {
+hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, bool shared_cu, bool kv8, hipStream_t stream) {
+  if (kv8) {  // fp8 pools: head dims that are whole 64-dim stripe rounds
+    switch (hd) {
+      case 64: return dispatch_tpp<DT, 64, true>(p, tpp, shared_cu, stream);
+      case 128: return dispatch_tpp<DT, 128, true>(p, tpp, shared_cu, stream);
+      case 256: return dispatch_tpp<DT, 256, true>(p, tpp, shared_cu, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (hd) {
-    case 32: return dispatch_tpp<DT, 32>(p, tpp, shared_cu, stream);
-    case 64: return dispatch_tpp<DT, 64>(p, tpp, shared_cu, stream);
-    case 80: return dispatch_tpp<DT, 80>(p, tpp, shared_cu, stream);
-    case 96: return dispatch_tpp<DT, 96>(p, tpp, shared_cu, stream);
-    case 128: return dispatch_tpp<DT, 128>(p, tpp, shared_cu, stream);
-    case 256: return dispatch_tpp<DT, 256>(p, tpp, shared_cu, stream);
+    case 32: return dispatch_tpp<DT, 32, false>(p, tpp, shared_cu, stream);
+    case 64: return dispatch_tpp<DT, 64, false>(p, tpp, shared_cu, stream);
+    case 80: return dispatch_tpp<DT, 80, false>(p, tpp, shared_cu, stream);
+    case 96: return dispatch_tpp<DT, 96, false>(p, tpp, shared_cu, stream);
+    case 128: return dispatch_tpp<DT, 128, false>(p, tpp, shared_cu, stream);
+    case 256: return dispatch_tpp<DT, 256, false>(p, tpp, shared_cu, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-template <int DT, int HD, int TPP>
+template <int DT, int HD, int TPP, bool KV8>
 const void* stream_kernel_ptr(bool chunks) {
-  return chunks ? reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP, true>)
-                : reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP, false>);
+  return chunks ? reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP, true, KV8>)
+                : reinterpret_cast<const void*>(&decode_stream_kernel<DT, HD, TPP, false, KV8>);
+}
+
+template <int DT, int HD, bool KV8>
+const void* stream_kernel_tpp(int tpp, bool chunks) {
+  return tpp == 32 ? stream_kernel_ptr<DT, HD, 32, KV8>(chunks) : stream_kernel_ptr<DT, HD, 16, KV8>(chunks);
 }
 
 template <int DT>
-const void* stream_kernel_for(int hd, int tpp, bool chunks) {
-  const bool t32 = tpp == 32;
+const void* stream_kernel_for(int hd, int tpp, bool chunks, bool kv8) {
+  if (kv8) {
+    switch (hd) {
+      case 64: return stream_kernel_tpp<DT, 64, true>(tpp, chunks);
+      case 128: return stream_kernel_tpp<DT, 128, true>(tpp, chunks);
+      case 256: return stream_kernel_tpp<DT, 256, true>(tpp, chunks);
+      default: return nullptr;
+    }
+  }
   switch (hd) {
-    case 32: return t32 ? stream_kernel_ptr<DT, 32, 32>(chunks) : stream_kernel_ptr<DT, 32, 16>(chunks);
-    case 64: return t32 ? stream_kernel_ptr<DT, 64, 32>(chunks) : stream_kernel_ptr<DT, 64, 16>(chunks);
-    case 80: return t32 ? stream_kernel_ptr<DT, 80, 32>(chunks) : stream_kernel_ptr<DT, 80, 16>(chunks);
-    case 96: return t32 ? stream_kernel_ptr<DT, 96, 32>(chunks) : stream_kernel_ptr<DT, 96, 16>(chunks);
-    case 128: return t32 ? stream_kernel_ptr<DT, 128, 32>(chunks) : stream_kernel_ptr<DT, 128, 16>(chunks);
-    case 256: return t32 ? stream_kernel_ptr<DT, 256, 32>(chunks) : stream_kernel_ptr<DT, 256, 16>(chunks);
+    case 32: return stream_kernel_tpp<DT, 32, false>(tpp, chunks);
+    case 64: return stream_kernel_tpp<DT, 64, false>(tpp, chunks);
+    case 80: return stream_kernel_tpp<DT, 80, false>(tpp, chunks);
+    case 96: return stream_kernel_tpp<DT, 96, false>(tpp, chunks);
+    case 128: return stream_kernel_tpp<DT, 128, false>(tpp, chunks);
+    case 256: return stream_kernel_tpp<DT, 256, false>(tpp, chunks);
     default: return nullptr;
   }
 }
@@ -1023,7 +1095,7 @@ const void* stream_kernel_for(int hd, int tpp, bool chunks) {
 }  // namespace
 
 hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, bool chunks,
-                                   int* workers) {
+                                   bool kv8, int* workers) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
@@ -1032,7 +1104,7 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
   const bool shared = shared_cu && shares_cu(head_dim);
   const uint64_t key = (static_cast<uint64_t>(dev) << 32) | (static_cast<uint64_t>(dtype & 0xff) << 24) |
                        (static_cast<uint64_t>(head_dim & 0xfff) << 12) | (static_cast<uint64_t>(tokens_per_page & 0xff) << 4) |
-                       (shared ? 2u : 0u) | (chunks ? 1u : 0u);
+                       (kv8 ? 4u : 0u) | (shared ? 2u : 0u) | (chunks ? 1u : 0u);
   static std::mutex mu;
   static std::unordered_map<uint64_t, int> cache;
   {
@@ -1050,8 +1122,8 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
   if (shared) {  // one workgroup per CU; the prefill tiles take the rest
     res = cus * kWorkersPerGroup;
   } else {
-    const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page, chunks)
-                                    : stream_kernel_for<kF16>(head_dim, tokens_per_page, chunks);
+    const void* fn = dtype == kBF16 ? stream_kernel_for<kBF16>(head_dim, tokens_per_page, chunks, kv8)
+                                    : stream_kernel_for<kF16>(head_dim, tokens_per_page, chunks, kv8);
     if (!fn) return hipErrorInvalidValue;
     int groups_per_cu = 0;
     err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kGroupThreads, 0);
@@ -1078,8 +1150,9 @@ int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partiti
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
                          hipStream_t stream) {
-  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, shared_cu, stream);
-  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, shared_cu, stream);
+  const bool kv8 = p.k_scales != nullptr;
+  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, shared_cu, kv8, stream);
+  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, shared_cu, kv8, stream);
 }
 
 }  // namespace pal

@@ -1,20 +1,40 @@
-// fill_kv_pages for gfx950: bit-exact scatter of new K/V rows into the pools.
+// fill_kv_pages for gfx950: scatter of new K/V rows into the paged pools,
+// optionally fused with the step that produces them (rotary position
+// embedding of K, and of Q, plus the cast from the projection's fp32 or
+// 16-bit output to the pool dtype, fp8 e4m3 pages quantized with
+// per-(page, kv head) scales included).
 //
 // Reference behaviour: kernels/paged_attention/fill_kv_pages.h.metal:65-116 --
 //   seq = q2seq[t], pos = write_pos[t], page = page_table[seq, pos / TPP],
 //   slot = pos % TPP,
-//   K[page, h, d / 8, slot, d % 8] = new_k[t, h, d]
+//   K[page, h, d / x, slot, d % x] = new_k[t, h, d]   (x = 16 / sizeof(element))
 //   V[page, h, d, slot]            = new_v[t, h, d]
+// a bit-exact copy when source and pool share the 16-bit dtype.
 //
-// Design (MI355X): the scatter is HBM-bound byte movement, so the mapping is
-// chosen for write coalescing and for parallelism at small token counts.
-// Workgroup (x, y) of 256 threads owns 16 consecutive tokens and 16 of their
-// 16-byte vectors (8 dims of one head each): thread (t = tid % 16,
-// v = 16 y + tid / 16) moves vector v of token 16 x + t, so even a 64-token
-// decode fill spreads over 32 workgroups.  When consecutive tokens
-// land in consecutive slots of a page (prefill chunks), the 16 lanes that
-// share v write 16 x 16 B = 256 contiguous bytes of K and, for each of the 8
-// dims, 16 x 2 B = 32 contiguous bytes of V.  Reads are whole 16-byte vectors.
+// Design (MI355X): HBM-bound byte movement, so the mapping is chosen for
+// whole-line writes and short dependency chains.  Workgroup (w, h) owns a
+// window of 64 consecutive new tokens (16 for small batches) and kv head h.
+// Its threads issue all their source loads first; meanwhile the first
+// threads resolve every token's destination (page, slot) into LDS.
+//  * K: a token's 8-dim chunk is one 16-byte stripe (16-bit pools) or half of
+//    one (fp8), and consecutive slots of a page are consecutive stripes, so
+//    lane i of a wavefront moves chunk c of token i: a prefill run writes
+//    whole lines.
+//  * V: row d of a (page, head) block holds the page's slots side by side, so
+//    one token's value is a 2-byte (1-byte) piece of a row.  Wherever 8
+//    consecutive window tokens fill an 8-aligned run of slots of one page
+//    (a prefill chunk), their converted V rows are staged in LDS and a
+//    thread gathers element d of the 8 tokens into one 16-byte (8-byte)
+//    store of row d; the remaining tokens (decode fills, the ragged ends of
+//    runs) are written element by element.
+//  * RoPE: position = the token's write position; cos / sin come from the
+//    caller's table [rows, rotary_dim] (cos of the rotary_dim / 2
+//    frequencies, then their sin).  NeoX style pairs dims (f, f + rot/2);
+//    GPT-J style pairs (2f, 2f + 1).  The products are rounded as written
+//    (no fused multiply-add), so results are bit-exact against a scalar fp32
+//    restatement.
+//  * fp8: q = x / scale[page, h], held to [-448, 448] (NaN stays NaN), then
+//    rounded to nearest even e4m3.
 // Tokens whose destination falls outside the page table or the pool are
 // skipped (the reference does not check and would write out of bounds).
 #include "pal_device.h"
@@ -23,36 +43,520 @@ namespace pal {
 
 namespace {
 
-constexpr int kFillTokens = 16;
-constexpr int kFillThreads = 256;
+#ifndef PAL_FILL_THREADS
+#define PAL_FILL_THREADS 256
+#endif
+constexpr int kThreads = PAL_FILL_THREADS;
+#ifndef PAL_FILL_LARGE_WIN
+#define PAL_FILL_LARGE_WIN 64
+#endif
+#ifndef PAL_FILL_SMALL_WIN
+#define PAL_FILL_SMALL_WIN 16
+#endif
+constexpr int kSmallWin = PAL_FILL_SMALL_WIN;
+constexpr int kLargeWin = PAL_FILL_LARGE_WIN;  // window of prefill-sized batches (16 for small ones)
+constexpr int kRowPad = 16;      // LDS row padding (bytes) of the staged K / V rows
 
-__global__ __launch_bounds__(kFillThreads) void fill_kv_pages_kernel(const FillParams p) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kFillTokens + (threadIdx.x % kFillTokens);
-  const int hd = p.head_dim;
-  const int stripes = hd / 8;
-  const int v = blockIdx.y * (kFillThreads / kFillTokens) + threadIdx.x / kFillTokens;
-  if (t >= p.num_tokens || v >= p.num_kv_heads * stripes) return;  // no barriers in this kernel
-  const uint32_t seq = p.q2seq[t];
-  const int32_t pos = p.write_pos[t];
-  const int tpp = p.tokens_per_page;
-  if (seq >= p.num_seqs || pos < 0 || pos / tpp >= p.page_table_width) return;
-  const uint32_t page = p.page_table[static_cast<int64_t>(seq) * p.page_table_width + pos / tpp];
-  if (page >= p.num_pages) return;
-  const int slot = pos % tpp;
+// ---- source element access: 8 consecutive values as fp32 -------------------
+template <int SRC>
+__device__ __forceinline__ void load8(const void* base, int64_t elem, float (&x)[8]) {
+  if constexpr (SRC == kF32) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = b[e];
+    }
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + elem);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = Dt<SRC>::to_f32(static_cast<uint16_t>(w[e] & 0xFFFFu));
+      x[2 * e + 1] = Dt<SRC>::to_f32(static_cast<uint16_t>(w[e] >> 16));
+    }
+  }
+}
 
-  const int h = v / stripes;
-  const int c = v - h * stripes;
-  const int64_t row = t * p.num_kv_heads * hd;
-  const u32x4 kd = reinterpret_cast<const u32x4*>(p.new_k + row)[v];
-  const u32x4 vd = reinterpret_cast<const u32x4*>(p.new_v + row)[v];
-  const int64_t head_block = static_cast<int64_t>(hd) * tpp;
-  const int64_t hb = (static_cast<int64_t>(page) * p.num_kv_heads + h) * head_block;
-  *reinterpret_cast<u32x4*>(p.k_pool + hb + (static_cast<int64_t>(c) * tpp + slot) * 8) = kd;
-  uint16_t* vdst = p.v_pool + hb + static_cast<int64_t>(c) * 8 * tpp + slot;
+// ---- destination encodings ---------------------------------------------------
+// fp8 e4m3 (OCP "fn" variant): x / scale held to the finite range, round to
+// nearest even (v_cvt_pk_fp8_f32).
+__device__ __forceinline__ float fp8_prescale(float x, float scale) {
+  float q = x / scale;  // correctly rounded division
+  q = q > 448.f ? 448.f : q;
+  q = q < -448.f ? -448.f : q;  // NaN compares false and stays NaN
+  return q;
+}
+__device__ __forceinline__ uint32_t fp8_pack4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return static_cast<uint32_t>(w);
+}
+
+template <int DST>
+struct Store8;
+template <>
+struct Store8<kF16> {
+  using T = u32x4;
+  static __device__ __forceinline__ T pack(const float (&x)[8], float) {
+    return T{Dt<kF16>::pack2(x[0], x[1]), Dt<kF16>::pack2(x[2], x[3]), Dt<kF16>::pack2(x[4], x[5]),
+             Dt<kF16>::pack2(x[6], x[7])};
+  }
+};
+template <>
+struct Store8<kBF16> {
+  using T = u32x4;
+  static __device__ __forceinline__ T pack(const float (&x)[8], float) {
+    return T{Dt<kBF16>::pack2(x[0], x[1]), Dt<kBF16>::pack2(x[2], x[3]), Dt<kBF16>::pack2(x[4], x[5]),
+             Dt<kBF16>::pack2(x[6], x[7])};
+  }
+};
+template <>
+struct Store8<kFP8> {
+  using T = u32x2;
+  static __device__ __forceinline__ T pack(const float (&x)[8], float scale) {
+    float q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = fp8_prescale(x[e], scale);
+    return T{fp8_pack4(q[0], q[1], q[2], q[3]), fp8_pack4(q[4], q[5], q[6], q[7])};
+  }
+};
+
+template <int DST>
+constexpr int elem_bytes() { return DST == kFP8 ? 1 : 2; }
+
+// Rotates the 8 values of chunk `lo` (dims d0..d0+7) with their partners:
+// NeoX: chunk `hi` holds dims d0 + rot/2 ..; GPT-J: pairs inside the chunk.
+// cs: the position's row of the cos/sin table.
+#pragma clang fp contract(off)
+__device__ __forceinline__ void rope_neox(float (&lo)[8], float (&hi)[8], const float* cs, int f0, int half) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = cs[f0 + e];
+    const float s = cs[half + f0 + e];
+    const float a = lo[e], b = hi[e];
+    lo[e] = a * c - b * s;
+    hi[e] = b * c + a * s;
+  }
+}
+__device__ __forceinline__ void rope_gptj(float (&x)[8], const float* cs, int f0, int half) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    vdst[(2 * e) * tpp] = static_cast<uint16_t>(vd[e] & 0xFFFFu);
-    vdst[(2 * e + 1) * tpp] = static_cast<uint16_t>(vd[e] >> 16);
+    const float c = cs[f0 + e];
+    const float s = cs[half + f0 + e];
+    const float a = x[2 * e], b = x[2 * e + 1];
+    x[2 * e] = a * c - b * s;
+    x[2 * e + 1] = b * c + a * s;
+  }
+}
+#pragma clang fp contract(on)
+
+// Stores chunk c (dims 8c..8c+7) of a token at `slot` of the K block that
+// starts `hb` bytes into the pool.
+template <int DST>
+__device__ __forceinline__ void store_k_chunk(const FillParams& p, int64_t hb, int slot, int c,
+                                              const typename Store8<DST>::T& v) {
+  const int64_t tpp = p.tokens_per_page;
+  uint8_t* base = static_cast<uint8_t*>(p.k_pool) + hb;
+  if constexpr (DST == kFP8) {  // stripes of 16 dims: chunk c is half of stripe c / 2
+    *reinterpret_cast<u32x2*>(base + ((c >> 1) * tpp + slot) * 16 + (c & 1) * 8) = v;
+  } else {  // stripes of 8 dims
+    *reinterpret_cast<u32x4*>(base + (c * tpp + slot) * 16) = v;
+  }
+}
+
+// Source rows of 8 values as loaded: raw 16-bit words, or fp32.
+template <int SRC>
+struct Raw8 {
+  u32x4 w;
+  __device__ __forceinline__ void load(const void* base, int64_t elem) {
+    w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + elem);
+  }
+  __device__ __forceinline__ void to_f32(float (&x)[8]) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = Dt<SRC>::to_f32(static_cast<uint16_t>(w[e] & 0xFFFFu));
+      x[2 * e + 1] = Dt<SRC>::to_f32(static_cast<uint16_t>(w[e] >> 16));
+    }
+  }
+};
+template <>
+struct Raw8<kF32> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const void* base, int64_t elem) {
+    a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem);
+    b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + elem + 4);
+  }
+  __device__ __forceinline__ void to_f32(float (&x)[8]) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = b[e];
+    }
+  }
+};
+
+// K work unit u of a row: NeoX rotation pairs chunk c with c + rot/16, so
+// unit u < rot/16 is that pair; every other unit is one chunk.  Without
+// NeoX pairs every unit is one chunk.
+__device__ __forceinline__ int k_units(const FillParams& p) {
+  return p.rope_style == 1 ? p.head_dim / 8 - p.rotary_dim / 16 : p.head_dim / 8;
+}
+__device__ __forceinline__ void unit_chunks(const FillParams& p, int u, int& c0, int& c1) {
+  if (p.rope_style == 1) {
+    const int pairs = p.rotary_dim / 16;
+    if (u < pairs) {
+      c0 = u;
+      c1 = u + pairs;
+    } else {
+      c0 = u + pairs;  // chunks at and past rotary_dim
+      c1 = -1;
+    }
+  } else {
+    c0 = u;
+    c1 = -1;
+  }
+}
+
+// Rotates the unit's chunk(s) in place (x: chunk c0, y: chunk c1 of a NeoX
+// pair) with row `pos` of the table, when rotate.
+__device__ __forceinline__ void rotate_unit(const FillParams& p, int c0, int c1, int pos, bool rotate, float (&x)[8],
+                                            float (&y)[8]) {
+  if (!rotate || p.rope_style == 0 || 8 * c0 >= p.rotary_dim) return;
+  const float* cs = p.cos_sin + static_cast<int64_t>(pos) * p.rotary_dim;
+  const int half = p.rotary_dim / 2;
+  if (p.rope_style == 1 && c1 >= 0) {
+    rope_neox(x, y, cs, 8 * c0, half);
+  } else if (p.rope_style == 2) {
+    rope_gptj(x, cs, 4 * c0, half);
+  }
+}
+
+// Workgroup (w, y) of the grid: y < Hkv moves K and V of kv head y for the
+// window of WIN new tokens w * WIN ..; y >= Hkv (rope with queries only)
+// rotates and casts query head y - Hkv of the window.  Each thread first
+// issues the loads of all its source chunks, chunks fastest so that a
+// wavefront reads whole lines of the source rows; meanwhile the first
+// wavefront resolves the destinations and classifies the window's tokens:
+// a token inside a full run of 8 slots of one page, or a single token.  A
+// single token's K chunks and V values are stored straight from registers.
+// Run tokens' rows go through LDS, and each run is then written in whole
+// lines: K stripe q of its 8 slots (8 x 16
+// contiguous bytes) and V row d of its 8 slots, the two runs of one page
+// side by side in neighbouring lanes.
+template <int SRC, int DST, int WIN, int MAXC>
+__global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParams p) {
+  constexpr int kItems = (WIN * MAXC + kThreads - 1) / kThreads;  // source chunks per thread, at most
+  constexpr int EB = elem_bytes<DST>();
+  static_assert(WIN <= kWave, "the first wavefront classifies the window");
+  // dynamic LDS: the run tokens' K or V rows, [WIN][HD * EB + kRowPad] bytes
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  __shared__ uint32_t page_lds[WIN];  // destination page of each window token
+  __shared__ int slot_lds[WIN];       // its slot, or -1: no valid destination
+  __shared__ int pos_lds[WIN];
+  __shared__ float ks_lds[WIN], vs_lds[WIN];  // fp8 scales of each token's (page, head)
+  __shared__ int kind_lds[WIN];       // 0: nothing to write, 1: single token, 2: in a full run
+  __shared__ int run_lds[WIN / 8];    // window index of each full run's first token
+  __shared__ int n_runs_lds;
+  const int hd = p.head_dim;
+  const int tpp = p.tokens_per_page;
+  const int chunks = hd / 8;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * WIN;
+  const int tid = threadIdx.x;
+  const int nwin = static_cast<int>(min(static_cast<int64_t>(WIN), p.num_tokens - t0));
+  const int units = k_units(p);
+
+  if (static_cast<int>(blockIdx.y) >= 2 * p.num_kv_heads) {
+    // ---- queries: rotate and cast head qh of the window's rows (a row is
+    // contiguous in and out, so units run fastest: whole lines per wave)
+    const int qh = blockIdx.y - 2 * p.num_kv_heads;
+    const int64_t q_row = static_cast<int64_t>(p.num_q_heads) * hd;
+    Raw8<SRC> rx[kItems], ry[kItems];
+    int pos[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const int it = tid + k * kThreads;
+      const int i = it / units;
+      if (i < nwin) {
+        int c0, c1;
+        unit_chunks(p, it % units, c0, c1);
+        const int64_t row = (t0 + i) * q_row + static_cast<int64_t>(qh) * hd;
+        rx[k].load(p.q_in, row + 8 * c0);
+        if (c1 >= 0) ry[k].load(p.q_in, row + 8 * c1);
+        pos[k] = p.write_pos[t0 + i];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const int it = tid + k * kThreads;
+      const int i = it / units;
+      if (i >= nwin) continue;
+      int c0, c1;
+      unit_chunks(p, it % units, c0, c1);
+      float x[8], y[8];
+      rx[k].to_f32(x);
+      if (c1 >= 0) ry[k].to_f32(y);
+      rotate_unit(p, c0, c1, pos[k], pos[k] >= 0 && pos[k] < p.cos_sin_rows, x, y);
+      uint16_t* qo = static_cast<uint16_t*>(p.q_out) + (t0 + i) * q_row + static_cast<int64_t>(qh) * hd;
+      if (p.q_out_dtype == kBF16) {
+        *reinterpret_cast<u32x4*>(qo + 8 * c0) = Store8<kBF16>::pack(x, 1.f);
+        if (c1 >= 0) *reinterpret_cast<u32x4*>(qo + 8 * c1) = Store8<kBF16>::pack(y, 1.f);
+      } else {
+        *reinterpret_cast<u32x4*>(qo + 8 * c0) = Store8<kF16>::pack(x, 1.f);
+        if (c1 >= 0) *reinterpret_cast<u32x4*>(qo + 8 * c1) = Store8<kF16>::pack(y, 1.f);
+      }
+    }
+    return;
+  }
+
+  // K workgroups (y < Hkv) and V workgroups (Hkv <= y < 2 Hkv) of kv head h
+  const bool is_k = static_cast<int>(blockIdx.y) < p.num_kv_heads;
+  const int h = is_k ? blockIdx.y : blockIdx.y - p.num_kv_heads;
+  const int64_t k_row = static_cast<int64_t>(p.num_kv_heads) * hd;  // source elements per token
+  const int krow_bytes = hd * EB;                                    // one token's K or V row
+  const int lrow = krow_bytes + kRowPad;                             // its LDS row stride
+  uint8_t* k_lds = dyn_lds;
+  uint8_t* v_lds = dyn_lds;
+  // ---- issue every source load of this thread (K units or V chunks; chunks fastest)
+  Raw8<SRC> kx[kItems], ky[kItems];
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    const int it = tid + k * kThreads;
+    if (is_k) {
+      const int i = it / units;
+      if (i < nwin) {
+        int c0, c1;
+        unit_chunks(p, it % units, c0, c1);
+        const int64_t row = (t0 + i) * k_row + static_cast<int64_t>(h) * hd;
+        kx[k].load(p.new_k, row + 8 * c0);
+        if (c1 >= 0) ky[k].load(p.new_k, row + 8 * c1);
+      }
+    } else {
+      const int i = it / chunks;
+      if (i < nwin) kx[k].load(p.new_v, (t0 + i) * k_row + static_cast<int64_t>(h) * hd + 8 * (it % chunks));
+    }
+  }
+  // ---- destinations (two dependent loads: the map, then the page table)
+  if (tid < WIN) {
+    uint32_t dpage = 0;
+    int dslot = -1;
+    int pos = 0;
+    float ks = 1.f, vs = 1.f;
+    if (tid < nwin) {
+      const int64_t t = t0 + tid;
+      const uint32_t seq = p.q2seq[t];
+      pos = p.write_pos[t];
+      if (seq < p.num_seqs && pos >= 0 && pos / tpp < p.page_table_width &&
+          (p.rope_style == 0 || pos < p.cos_sin_rows)) {
+        const uint32_t page = p.page_table[static_cast<int64_t>(seq) * p.page_table_width + pos / tpp];
+        if (page < p.num_pages) {
+          dpage = page;
+          dslot = pos % tpp;
+          if constexpr (DST == kFP8) {
+            ks = p.k_scales[static_cast<int64_t>(page) * p.num_kv_heads + h];
+            vs = p.v_scales[static_cast<int64_t>(page) * p.num_kv_heads + h];
+          }
+        }
+      }
+    }
+    page_lds[tid] = dpage;
+    slot_lds[tid] = dslot;
+    pos_lds[tid] = pos;
+    ks_lds[tid] = ks;
+    vs_lds[tid] = vs;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    // A full run: slots 8k..8k+7 of one page (pages of a multiple of 8
+    // slots, so the run's pieces of K stripes and V rows are aligned)
+    // written by 8 consecutive window tokens.  Token i lies in the run
+    // starting at j = i - slot % 8, if any.
+    auto is_lead = [&](int j) {
+      if (j < 0 || j + 8 > nwin || (tpp % 8) != 0) return false;
+      const int s0 = slot_lds[j];
+      if (s0 < 0 || s0 % 8 != 0) return false;
+      const uint32_t pg0 = page_lds[j];
+      for (int e = 1; e < 8; ++e)
+        if (slot_lds[j + e] != s0 + e || page_lds[j + e] != pg0) return false;
+      return true;
+    };
+    int kind = 0;
+    bool lead = false;
+    if (tid < nwin && slot_lds[tid] >= 0) {
+      lead = is_lead(tid);
+      kind = (lead || is_lead(tid - slot_lds[tid] % 8)) ? 2 : 1;
+    }
+    if (tid < WIN) kind_lds[tid] = kind;
+    const uint64_t leads = __ballot(lead);
+    if (lead) run_lds[__popcll(leads & ((1ull << tid) - 1))] = tid;
+    if (tid == 0) n_runs_lds = __popcll(leads);
+  }
+  __syncthreads();
+
+  const int64_t head_block = static_cast<int64_t>(hd) * tpp * EB;  // bytes per (page, kv head) block
+  // ---- single tokens to the pool, run tokens into LDS
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    const int it = tid + k * kThreads;
+    if (is_k) {  // K unit
+      const int i = it / units;
+      if (i < nwin && slot_lds[i] >= 0) {
+        int c0, c1;
+        unit_chunks(p, it % units, c0, c1);
+        typename Store8<DST>::T a, b;
+        bool copied = false;
+        if constexpr (SRC == DST) {
+          if (p.rope_style == 0) {  // the reference's fill: a bit copy (NaN payloads included)
+            a = kx[k].w;
+            copied = true;
+          }
+        }
+        if (!copied) {
+          float x[8], y[8];
+          kx[k].to_f32(x);
+          if (c1 >= 0) ky[k].to_f32(y);
+          rotate_unit(p, c0, c1, pos_lds[i], true, x, y);
+          a = Store8<DST>::pack(x, ks_lds[i]);
+          if (c1 >= 0) b = Store8<DST>::pack(y, ks_lds[i]);
+        }
+        if (kind_lds[i] == 1) {
+          const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
+          store_k_chunk<DST>(p, hb, slot_lds[i], c0, a);
+          if (c1 >= 0) store_k_chunk<DST>(p, hb, slot_lds[i], c1, b);
+        } else {
+          *reinterpret_cast<typename Store8<DST>::T*>(k_lds + i * lrow + c0 * 8 * EB) = a;
+          if (c1 >= 0) *reinterpret_cast<typename Store8<DST>::T*>(k_lds + i * lrow + c1 * 8 * EB) = b;
+        }
+      }
+    } else {  // V chunk
+      const int i = it / chunks;
+      const int c = it % chunks;
+      if (i < nwin && slot_lds[i] >= 0) {
+        // the chunk's 8 values as pool elements (16-bit, or fp8 bytes in the low byte)
+        uint32_t e16[8];
+        if constexpr (SRC == DST) {  // bit copy
+#pragma unroll
+          for (int e = 0; e < 8; ++e) e16[e] = (kx[k].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        } else {
+          float x[8];
+          kx[k].to_f32(x);
+          if constexpr (DST == kFP8) {
+            const u32x2 q = Store8<kFP8>::pack(x, vs_lds[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) e16[e] = (q[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+          } else {
+            const u32x4 q = Store8<DST>::pack(x, 1.f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) e16[e] = (q[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          }
+        }
+        if (kind_lds[i] == 1) {
+          const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
+          uint8_t* col = static_cast<uint8_t*>(p.v_pool) + hb + (static_cast<int64_t>(8 * c) * tpp + slot_lds[i]) * EB;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if constexpr (DST == kFP8) {
+              col[e * tpp] = static_cast<uint8_t>(e16[e]);
+            } else {
+              *reinterpret_cast<uint16_t*>(col + e * tpp * 2) = static_cast<uint16_t>(e16[e]);
+            }
+          }
+        } else {  // a run token: its chunk into LDS as it is
+          if constexpr (DST == kFP8) {
+            *reinterpret_cast<u32x2*>(v_lds + i * lrow + c * 8) =
+                u32x2{e16[0] | (e16[1] << 8) | (e16[2] << 16) | (e16[3] << 24),
+                      e16[4] | (e16[5] << 8) | (e16[6] << 16) | (e16[7] << 24)};
+          } else {
+            *reinterpret_cast<u32x4*>(v_lds + i * lrow + c * 16) =
+                u32x4{e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16)};
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const int n_runs = n_runs_lds;
+  if (n_runs == 0) return;
+  if (is_k) {
+    // ---- K of the runs: item = (stripe q, run r, slot j), slots fastest: 8
+    // lanes write the run's 128 contiguous bytes of stripe q (a stripe is 16
+    // bytes: 8 dims of 16-bit, 16 of fp8), and runs r, r+1 (often the two
+    // halves of one page) follow each other.
+    const int pieces = krow_bytes / 16;  // 16-byte pieces of a token's K row
+    for (int it = tid; it < pieces * n_runs * 8; it += kThreads) {
+      const int j = it % 8;
+      const int r = (it / 8) % n_runs;
+      const int q = it / (8 * n_runs);
+      const int i = run_lds[r] + j;
+      const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
+      // piece q is stripe q (16-bit: 8 dims, fp8: 16 dims) of the token
+      *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(p.k_pool) + hb + (static_cast<int64_t>(q) * tpp + slot_lds[i]) * 16) =
+          *reinterpret_cast<const u32x4*>(k_lds + i * lrow + q * 16);
+    }
+    return;
+  }
+  // ---- V of the runs: item = (row d, run r), runs fastest in pairs, so
+  // lanes 2d, 2d+1 write row d of two runs (a page's two halves side by
+  // side) and consecutive rows follow: whole lines per wavefront
+  for (int it = tid; it < hd * n_runs; it += kThreads) {
+    const int r = it % n_runs;
+    const int d = it / n_runs;
+    const int i = run_lds[r];
+    const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
+    uint8_t* row = static_cast<uint8_t*>(p.v_pool) + hb + (static_cast<int64_t>(d) * tpp + slot_lds[i]) * EB;
+    // element d of the run's 8 tokens (rows i .. i+7 in LDS)
+    const uint8_t* src = v_lds + i * lrow + d * EB;
+    if constexpr (DST == kFP8) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo |= static_cast<uint32_t>(src[e * lrow]) << (8 * e);
+        hi |= static_cast<uint32_t>(src[(4 + e) * lrow]) << (8 * e);
+      }
+      *reinterpret_cast<u32x2*>(row) = u32x2{lo, hi};
+    } else {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(src + 2 * e * lrow)) |
+               (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(src + (2 * e + 1) * lrow)) << 16);
+      *reinterpret_cast<u32x4*>(row) = w;
+    }
+  }
+}
+
+template <int SRC, int DST, int MAXC>
+hipError_t launch_win(const FillParams& p, hipStream_t stream) {
+  // small batches (decode fills): windows of 16 tokens, so a 64-token fill
+  // still spreads over 4 x 2 Hkv workgroups; prefill batches: 32
+  const int win = p.num_tokens >= 2048 ? kLargeWin : kSmallWin;
+  const int64_t windows = (p.num_tokens + win - 1) / win;
+  const unsigned gy = 2 * p.num_kv_heads + (p.q_in ? p.num_q_heads : 0);
+  const size_t lds = static_cast<size_t>(win) * (p.head_dim * elem_bytes<DST>() + kRowPad);  // K or V rows
+  if (win == kLargeWin)
+    hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kLargeWin, MAXC>), dim3(static_cast<unsigned>(windows), gy),
+                       dim3(kThreads), lds, stream, p);
+  else
+    hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kSmallWin, MAXC>), dim3(static_cast<unsigned>(windows), gy),
+                       dim3(kThreads), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int SRC, int DST>
+hipError_t launch_t(const FillParams& p, hipStream_t stream) {
+  // per-thread item registers sized for the head dim: up to 128 or up to 256
+  if (p.head_dim <= 128) return launch_win<SRC, DST, 16>(p, stream);
+  return launch_win<SRC, DST, kMaxFillHeadDim / 8>(p, stream);
+}
+
+template <int SRC>
+hipError_t launch_dst(const FillParams& p, hipStream_t stream) {
+  switch (p.kv_dtype) {
+    case kF16: return launch_t<SRC, kF16>(p, stream);
+    case kBF16: return launch_t<SRC, kBF16>(p, stream);
+    case kFP8: return launch_t<SRC, kFP8>(p, stream);
+    default: return hipErrorInvalidValue;
   }
 }
 
@@ -60,12 +564,13 @@ __global__ __launch_bounds__(kFillThreads) void fill_kv_pages_kernel(const FillP
 
 hipError_t launch_fill_kv_pages(const FillParams& p, hipStream_t stream) {
   if (p.num_tokens <= 0) return hipSuccess;
-  const int64_t blocks = (p.num_tokens + kFillTokens - 1) / kFillTokens;
-  const int nvec = p.num_kv_heads * (p.head_dim / 8);
-  const int vec_blocks = (nvec + kFillThreads / kFillTokens - 1) / (kFillThreads / kFillTokens);
-  hipLaunchKernelGGL(fill_kv_pages_kernel, dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(vec_blocks)),
-                     dim3(kFillThreads), 0, stream, p);
-  return hipGetLastError();
+  if (p.head_dim > kMaxFillHeadDim) return hipErrorInvalidValue;
+  switch (p.src_dtype) {
+    case kF16: return launch_dst<kF16>(p, stream);
+    case kBF16: return launch_dst<kBF16>(p, stream);
+    case kF32: return launch_dst<kF32>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace pal

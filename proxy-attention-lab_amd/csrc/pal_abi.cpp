@@ -42,6 +42,8 @@ int hip_status(hipError_t err, const char* what) {
 }
 
 bool valid_dtype(int dtype) { return dtype == PAL_DTYPE_FLOAT16 || dtype == PAL_DTYPE_BFLOAT16; }
+bool valid_pool_dtype(int dtype) { return valid_dtype(dtype) || dtype == PAL_DTYPE_FP8_E4M3; }
+int pool_elem_bytes(int dtype) { return dtype == PAL_DTYPE_FP8_E4M3 ? 1 : 2; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -93,11 +95,11 @@ DecodeLayout decode_layout(int64_t num_seqs, int head_dim, int hg_max, int64_t v
 // slots) the cut can produce: one per equal static share, or, with a
 // partition size, one per chunk of the page-table capacity.
 int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seqs, int num_kv_heads,
-                   int head_chunks, int64_t page_table_width, int partition_size, bool shared_cu, int* resident,
-                   int64_t* virtual_workers) {
+                   int head_chunks, int64_t page_table_width, int partition_size, bool shared_cu, bool kv8,
+                   int* resident, int64_t* virtual_workers) {
   int res = 0;
   hipError_t err =
-      pal::decode_resident_workers(dtype, head_dim, tokens_per_page, shared_cu, partition_size > 0, &res);
+      pal::decode_resident_workers(dtype, head_dim, tokens_per_page, shared_cu, partition_size > 0, kv8, &res);
   if (err != hipSuccess)
     return fail(PAL_ERR_HIP, "[paged_attention_decode] occupancy query failed: %s", hipGetErrorString(err));
   const int64_t max_blocks =
@@ -144,8 +146,10 @@ pal::DecodeParams decode_params(const void* queries, const void* k_pool, const v
   const int group = num_q_heads / num_kv_heads;
   pal::DecodeParams p;
   p.q = static_cast<const uint16_t*>(queries);
-  p.k_pool = static_cast<const uint16_t*>(k_pool);
-  p.v_pool = static_cast<const uint16_t*>(v_pool);
+  p.k_pool = k_pool;
+  p.v_pool = v_pool;
+  p.k_scales = nullptr;
+  p.v_scales = nullptr;
   p.page_table = page_table;
   p.seq_lens = sequence_lengths;
   p.out = static_cast<uint16_t*>(out);
@@ -188,15 +192,136 @@ int check_attention_dims(const char* op, int dtype, int num_q_heads, int num_kv_
   return PAL_OK;
 }
 
+size_t decode_workspace_size(int dtype, int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                             int tokens_per_page, int64_t page_table_width, int partition_size, bool kv8) {
+  if (!valid_dtype(dtype) || num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      tokens_per_page <= 0 || page_table_width < 0 || num_q_heads % num_kv_heads != 0 ||
+      !decode_partition_ok(partition_size) || !decode_head_dim_supported(head_dim) ||
+      (tokens_per_page != 16 && tokens_per_page != 32))
+    return 0;
+  const int group = num_q_heads / num_kv_heads;
+  const int chunks = (group + 15) / 16;
+  int resident = 0;
+  int64_t vw = 0;
+  if (decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
+                     partition_size, false, kv8, &resident, &vw) != PAL_OK)
+    return 0;
+  return decode_layout(num_seqs, head_dim, group < 16 ? group : 16, vw).total;
+}
+
+// Arguments of the three fill entry points (pal_fill_kv_pages,
+// pal_fill_kv_pages_fp8, pal_rope_fill_kv_pages), validated in one place.
+struct FillArgs {
+  const void* new_keys = nullptr;
+  const void* new_values = nullptr;
+  int src_dtype = -1;
+  void* k_pool = nullptr;
+  void* v_pool = nullptr;
+  int kv_dtype = -1;
+  const float* k_scales = nullptr;
+  const float* v_scales = nullptr;
+  const uint32_t* page_table = nullptr;
+  const int32_t* write_positions = nullptr;
+  const uint32_t* query_to_seq_map = nullptr;
+  int64_t num_tokens = 0;
+  int num_kv_heads = 0;
+  int head_dim = 0;
+  int tokens_per_page = 0;
+  int64_t num_pages = 0;
+  int64_t num_seqs = 0;
+  int64_t page_table_width = 0;
+  const float* cos_sin = nullptr;
+  int64_t cos_sin_rows = 0;
+  int rotary_dim = 0;
+  int rope_style = 0;
+  const void* queries = nullptr;
+  void* queries_out = nullptr;
+  int num_q_heads = 0;
+  int q_out_dtype = PAL_DTYPE_BFLOAT16;
+};
+
+int fill_call(const char* op, const FillArgs& a, hipStream_t stream) {
+  const bool fp8 = a.kv_dtype == PAL_DTYPE_FP8_E4M3;
+  if (!valid_dtype(a.kv_dtype) && !fp8) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] unsupported pool dtype code %d", op, a.kv_dtype);
+  if (!valid_dtype(a.src_dtype) && a.src_dtype != PAL_DTYPE_FLOAT32)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] unsupported source dtype code %d", op, a.src_dtype);
+  if (a.num_tokens < 0 || a.num_kv_heads <= 0 || a.head_dim <= 0 || a.tokens_per_page <= 0 || a.num_pages < 0 ||
+      a.num_seqs < 0 || a.page_table_width < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative or zero dimension", op);
+  const int chunk_dims = fp8 ? 16 : 8;  // one K stripe
+  if (a.head_dim % chunk_dims != 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] head_dim %d must be a multiple of %d", op, a.head_dim, chunk_dims);
+  if (a.head_dim > pal::kMaxFillHeadDim)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] head_dim %d above the supported %d", op, a.head_dim,
+                pal::kMaxFillHeadDim);
+  if (a.rope_style < 0 || a.rope_style > 2)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] rope_style %d not in {0 none, 1 neox, 2 gptj}", op, a.rope_style);
+  if (a.rope_style != 0) {
+    const int mult = a.rope_style == 1 ? 16 : 8;
+    if (a.rotary_dim <= 0 || a.rotary_dim > a.head_dim || a.rotary_dim % mult != 0)
+      return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] rotary_dim %d must be a positive multiple of %d up to head_dim %d",
+                  op, a.rotary_dim, mult, a.head_dim);
+    if (a.cos_sin_rows < 0 || (a.num_tokens > 0 && (!a.cos_sin || a.cos_sin_rows == 0)))
+      return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] rope needs a cos/sin table", op);
+  }
+  if (a.queries) {
+    if (a.rope_style == 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] queries given without rope", op);
+    if (!a.queries_out || !valid_dtype(a.q_out_dtype) || a.num_q_heads <= 0 || a.num_q_heads % a.num_kv_heads != 0)
+      return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] queries need an output, a 16-bit output dtype and num_q_heads a "
+                  "multiple of num_kv_heads", op);
+  }
+  if (a.num_tokens == 0) return ok();
+  if (!a.new_keys || !a.new_values || !a.k_pool || !a.v_pool || !a.page_table || !a.write_positions ||
+      !a.query_to_seq_map || (fp8 && (!a.k_scales || !a.v_scales)))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
+  if (!aligned16(a.new_keys) || !aligned16(a.new_values) || !aligned16(a.k_pool) || !aligned16(a.v_pool) ||
+      (a.queries && (!aligned16(a.queries) || !aligned16(a.queries_out))))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] new keys/values, pools and queries must be 16-byte aligned", op);
+  pal::FillParams p;
+  p.new_k = a.new_keys;
+  p.new_v = a.new_values;
+  p.k_pool = a.k_pool;
+  p.v_pool = a.v_pool;
+  p.k_scales = a.k_scales;
+  p.v_scales = a.v_scales;
+  p.page_table = a.page_table;
+  p.write_pos = a.write_positions;
+  p.q2seq = a.query_to_seq_map;
+  p.cos_sin = a.cos_sin;
+  p.q_in = a.queries;
+  p.q_out = a.queries_out;
+  p.num_tokens = a.num_tokens;
+  p.num_pages = a.num_pages;
+  p.num_seqs = a.num_seqs;
+  p.page_table_width = a.page_table_width;
+  p.cos_sin_rows = a.rope_style != 0 ? a.cos_sin_rows : 0;
+  p.num_kv_heads = a.num_kv_heads;
+  p.num_q_heads = a.num_q_heads;
+  p.head_dim = a.head_dim;
+  p.tokens_per_page = a.tokens_per_page;
+  p.src_dtype = a.src_dtype;
+  p.kv_dtype = a.kv_dtype;
+  p.q_out_dtype = a.q_out_dtype;
+  p.rope_style = a.rope_style;
+  p.rotary_dim = a.rope_style != 0 ? a.rotary_dim : 0;
+  return hip_status(pal::launch_fill_kv_pages(p, stream), op);
+}
+
 // pal_paged_attention_decode and its no-allocation variant: with
 // use_scratch the workspace is the library's per-device scratch array (no
 // caller buffer, nothing allocated), and calls needing more than it holds
 // are rejected.
-int decode_call(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
-                const int32_t* sequence_lengths, void* out, int dtype, int64_t num_query_rows, int64_t num_seqs,
-                int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
-                int64_t page_table_width, int partition_size, void* workspace, size_t workspace_bytes,
-                bool use_scratch, hipStream_t stream) {
+int decode_call(const void* queries, const void* k_pool, const void* v_pool, const float* k_scales,
+                const float* v_scales, const uint32_t* page_table, const int32_t* sequence_lengths, void* out,
+                int dtype, int64_t num_query_rows, int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                int tokens_per_page, int64_t num_pages, int64_t page_table_width, int partition_size,
+                void* workspace, size_t workspace_bytes, bool use_scratch, hipStream_t stream) {
+  const bool kv8 = k_scales != nullptr || v_scales != nullptr;
+  if (kv8 && (!k_scales || !v_scales))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] fp8 pools need both k_scales and v_scales");
+  if (kv8 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PAL_ERR_RUNTIME, "[paged_attention_decode] no fp8 kernel for head_dim %d (supported: 64, 128, 256)",
+                head_dim);
   if (!valid_dtype(dtype))
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] unsupported dtype code %d", dtype);
   if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
@@ -223,7 +348,7 @@ int decode_call(const void* queries, const void* k_pool, const void* v_pool, con
   int resident = 0;
   int64_t vw = 0;
   const int st = decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                                partition_size, false, &resident, &vw);
+                                partition_size, false, kv8, &resident, &vw);
   if (st != PAL_OK) return st;
   const DecodeLayout lay = decode_layout(num_seqs, head_dim, hg_max, vw);
   if (use_scratch) {
@@ -250,10 +375,11 @@ int decode_call(const void* queries, const void* k_pool, const void* v_pool, con
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] workspace must be 256-byte aligned");
 
-  const pal::DecodeParams p = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
-                                            static_cast<char*>(workspace), lay, num_seqs, num_pages,
-                                            page_table_width, num_q_heads, num_kv_heads, head_dim, resident,
-                                            partition_size);
+  pal::DecodeParams p = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
+                                      static_cast<char*>(workspace), lay, num_seqs, num_pages, page_table_width,
+                                      num_q_heads, num_kv_heads, head_dim, resident, partition_size);
+  p.k_scales = k_scales;
+  p.v_scales = v_scales;
   return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, false, stream),
                     "paged_attention_decode");
 }
@@ -267,17 +393,17 @@ const char* pal_last_error(void) { return g_last_error.c_str(); }
 const char* pal_version(void) { return "2025.06.4+gfx950"; }
 
 int pal_get_k_cache_stripe_size(int dtype) {
-  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
+  if (!valid_pool_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
   ok();
-  return 16 / 2;
+  return 16 / pool_elem_bytes(dtype);
 }
 
 int pal_get_optimal_page_size(void) { return 16; }
 
 int pal_get_k_cache_shape(int64_t num_pages, int num_kv_heads, int head_dim, int tokens_per_page,
                           int dtype, int64_t out_shape[5]) {
-  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
-  const int x = 8;
+  if (!valid_pool_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
+  const int x = 16 / pool_elem_bytes(dtype);
   out_shape[0] = num_pages;
   out_shape[1] = num_kv_heads;
   out_shape[2] = head_dim / x;
@@ -288,7 +414,7 @@ int pal_get_k_cache_shape(int64_t num_pages, int num_kv_heads, int head_dim, int
 
 int pal_get_v_cache_shape(int64_t num_pages, int num_kv_heads, int head_dim, int tokens_per_page,
                           int dtype, int64_t out_shape[4]) {
-  if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
+  if (!valid_pool_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "unsupported dtype code %d", dtype);
   out_shape[0] = num_pages;
   out_shape[1] = num_kv_heads;
   out_shape[2] = head_dim;
@@ -302,50 +428,103 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
                       int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
                       int64_t num_seqs, int64_t page_table_width, void* stream) {
   if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] unsupported dtype code %d", dtype);
-  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 ||
-      num_pages < 0 || num_seqs < 0 || page_table_width < 0)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] negative or zero dimension");
-  if (head_dim % 8 != 0)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] head_dim %d must be a multiple of 8", head_dim);
-  if (num_tokens == 0) return ok();
-  if (!new_keys || !new_values || !k_pool || !v_pool || !page_table || !write_positions || !query_to_seq_map)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] null pointer argument");
-  if (!aligned16(new_keys) || !aligned16(new_values) || !aligned16(k_pool))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[fill_kv_pages] new_keys, new_values and k_pool must be 16-byte aligned");
-  pal::FillParams p;
-  p.new_k = static_cast<const uint16_t*>(new_keys);
-  p.new_v = static_cast<const uint16_t*>(new_values);
-  p.k_pool = static_cast<uint16_t*>(k_pool);
-  p.v_pool = static_cast<uint16_t*>(v_pool);
-  p.page_table = page_table;
-  p.write_pos = write_positions;
-  p.q2seq = query_to_seq_map;
-  p.num_tokens = num_tokens;
-  p.num_pages = num_pages;
-  p.num_seqs = num_seqs;
-  p.page_table_width = page_table_width;
-  p.num_kv_heads = num_kv_heads;
-  p.head_dim = head_dim;
-  p.tokens_per_page = tokens_per_page;
-  return hip_status(pal::launch_fill_kv_pages(p, static_cast<hipStream_t>(stream)), "fill_kv_pages");
+  FillArgs a;
+  a.new_keys = new_keys;
+  a.new_values = new_values;
+  a.src_dtype = dtype;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.kv_dtype = dtype;
+  a.page_table = page_table;
+  a.write_positions = write_positions;
+  a.query_to_seq_map = query_to_seq_map;
+  a.num_tokens = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = head_dim;
+  a.tokens_per_page = tokens_per_page;
+  a.num_pages = num_pages;
+  a.num_seqs = num_seqs;
+  a.page_table_width = page_table_width;
+  return fill_call("fill_kv_pages", a, static_cast<hipStream_t>(stream));
+}
+
+int pal_fill_kv_pages_fp8(const void* new_keys, const void* new_values, int src_dtype, void* k_pool, void* v_pool,
+                          const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                          const int32_t* write_positions, const uint32_t* query_to_seq_map, int64_t num_tokens,
+                          int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages, int64_t num_seqs,
+                          int64_t page_table_width, void* stream) {
+  FillArgs a;
+  a.new_keys = new_keys;
+  a.new_values = new_values;
+  a.src_dtype = src_dtype;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.kv_dtype = PAL_DTYPE_FP8_E4M3;
+  a.k_scales = k_scales;
+  a.v_scales = v_scales;
+  a.page_table = page_table;
+  a.write_positions = write_positions;
+  a.query_to_seq_map = query_to_seq_map;
+  a.num_tokens = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = head_dim;
+  a.tokens_per_page = tokens_per_page;
+  a.num_pages = num_pages;
+  a.num_seqs = num_seqs;
+  a.page_table_width = page_table_width;
+  return fill_call("fill_kv_pages_fp8", a, static_cast<hipStream_t>(stream));
+}
+
+int pal_rope_fill_kv_pages(const void* new_keys, const void* new_values, int src_dtype, void* k_pool, void* v_pool,
+                           int kv_dtype, const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                           const int32_t* write_positions, const uint32_t* query_to_seq_map, int64_t num_tokens,
+                           int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages, int64_t num_seqs,
+                           int64_t page_table_width, const float* cos_sin_cache, int64_t cos_sin_rows,
+                           int rotary_dim, int rope_style, const void* queries, void* queries_out,
+                           int num_q_heads, int q_out_dtype, void* stream) {
+  FillArgs a;
+  a.new_keys = new_keys;
+  a.new_values = new_values;
+  a.src_dtype = src_dtype;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.kv_dtype = kv_dtype;
+  a.k_scales = k_scales;
+  a.v_scales = v_scales;
+  a.page_table = page_table;
+  a.write_positions = write_positions;
+  a.query_to_seq_map = query_to_seq_map;
+  a.num_tokens = num_tokens;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = head_dim;
+  a.tokens_per_page = tokens_per_page;
+  a.num_pages = num_pages;
+  a.num_seqs = num_seqs;
+  a.page_table_width = page_table_width;
+  a.cos_sin = cos_sin_cache;
+  a.cos_sin_rows = cos_sin_rows;
+  a.rotary_dim = rotary_dim;
+  a.rope_style = rope_style;
+  a.queries = queries;
+  a.queries_out = queries_out;
+  a.num_q_heads = num_q_heads;
+  a.q_out_dtype = q_out_dtype;
+  return fill_call("rope_fill_kv_pages", a, static_cast<hipStream_t>(stream));
 }
 
 size_t pal_paged_attention_decode_workspace_size(int dtype, int64_t num_seqs, int num_q_heads,
                                                  int num_kv_heads, int head_dim, int tokens_per_page,
                                                  int64_t page_table_width, int partition_size) {
-  if (!valid_dtype(dtype) || num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
-      tokens_per_page <= 0 || page_table_width < 0 || num_q_heads % num_kv_heads != 0 ||
-      !decode_partition_ok(partition_size) || !decode_head_dim_supported(head_dim) ||
-      (tokens_per_page != 16 && tokens_per_page != 32))
-    return 0;
-  const int group = num_q_heads / num_kv_heads;
-  const int chunks = (group + 15) / 16;
-  int resident = 0;
-  int64_t vw = 0;
-  if (decode_workers(dtype, head_dim, tokens_per_page, num_seqs, num_kv_heads, chunks, page_table_width,
-                     partition_size, false, &resident, &vw) != PAL_OK)
-    return 0;
-  return decode_layout(num_seqs, head_dim, group < 16 ? group : 16, vw).total;
+  return decode_workspace_size(dtype, num_seqs, num_q_heads, num_kv_heads, head_dim, tokens_per_page,
+                               page_table_width, partition_size, false);
+}
+
+size_t pal_paged_attention_decode_fp8_workspace_size(int dtype, int64_t num_seqs, int num_q_heads, int num_kv_heads,
+                                                     int head_dim, int tokens_per_page, int64_t page_table_width,
+                                                     int partition_size) {
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
+  return decode_workspace_size(dtype, num_seqs, num_q_heads, num_kv_heads, head_dim, tokens_per_page,
+                               page_table_width, partition_size, true);
 }
 
 int pal_paged_attention_decode(const void* queries, const void* k_pool, const void* v_pool,
@@ -355,9 +534,10 @@ int pal_paged_attention_decode(const void* queries, const void* k_pool, const vo
                                int tokens_per_page, int64_t num_pages, int64_t page_table_width,
                                int partition_size, void* workspace, size_t workspace_bytes,
                                void* stream) {
-  return decode_call(queries, k_pool, v_pool, page_table, sequence_lengths, out, dtype, num_query_rows, num_seqs,
-                     num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages, page_table_width,
-                     partition_size, workspace, workspace_bytes, false, static_cast<hipStream_t>(stream));
+  return decode_call(queries, k_pool, v_pool, nullptr, nullptr, page_table, sequence_lengths, out, dtype,
+                     num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                     page_table_width, partition_size, workspace, workspace_bytes, false,
+                     static_cast<hipStream_t>(stream));
 }
 
 int pal_paged_attention_decode_noalloc(const void* queries, const void* k_pool, const void* v_pool,
@@ -365,9 +545,23 @@ int pal_paged_attention_decode_noalloc(const void* queries, const void* k_pool, 
                                        int dtype, int64_t num_query_rows, int64_t num_seqs, int num_q_heads,
                                        int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
                                        int64_t page_table_width, int partition_size, void* stream) {
-  return decode_call(queries, k_pool, v_pool, page_table, sequence_lengths, out, dtype, num_query_rows, num_seqs,
-                     num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages, page_table_width,
-                     partition_size, nullptr, 0, true, static_cast<hipStream_t>(stream));
+  return decode_call(queries, k_pool, v_pool, nullptr, nullptr, page_table, sequence_lengths, out, dtype,
+                     num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                     page_table_width, partition_size, nullptr, 0, true, static_cast<hipStream_t>(stream));
+}
+
+int pal_paged_attention_decode_fp8(const void* queries, const void* k_pool, const void* v_pool,
+                                   const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                                   const int32_t* sequence_lengths, void* out, int dtype, int64_t num_query_rows,
+                                   int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                   int tokens_per_page, int64_t num_pages, int64_t page_table_width,
+                                   int partition_size, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!k_scales || !v_scales)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_decode] fp8 pools need both k_scales and v_scales");
+  return decode_call(queries, k_pool, v_pool, k_scales, v_scales, page_table, sequence_lengths, out, dtype,
+                     num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                     page_table_width, partition_size, workspace, workspace_bytes, false,
+                     static_cast<hipStream_t>(stream));
 }
 
 int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, const void* v_prompt,
@@ -437,7 +631,7 @@ size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int
   int resident = 0;
   int64_t vw = 0;
   if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
-                     true, &resident, &vw) != PAL_OK)
+                     true, false, &resident, &vw) != PAL_OK)
     return 0;
   return decode_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
 }
@@ -469,7 +663,8 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
   const int chunks = (group + 15) / 16;
   int resident = 0;
   int64_t vw = 0;
-  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, true, &resident,
+  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, true, false,
+                      &resident,
                       &vw);
   if (st != PAL_OK) return st;
   const DecodeLayout lay = decode_layout(num_query_rows, head_dim, hg_max, vw);

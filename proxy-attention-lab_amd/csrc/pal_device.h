@@ -61,6 +61,13 @@ struct Dt<kBF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // two fp8 e4m3 values (bytes 0-1, or 2-3 when hi) of w as a packed pair;
+  // exact: every e4m3 value is a bf16 value
+  static __device__ __forceinline__ uint32_t fp8x2(uint32_t w, bool hi) {
+    const f32x2 f = hi ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true)
+                       : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    return pack2(f[0], f[1]);
+  }
 };
 
 template <>
@@ -86,6 +93,13 @@ struct Dt<kF16> {
   static __device__ __forceinline__ f32x16 mma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // two fp8 e4m3 values as a packed pair; exact (e4m3's range and 3-bit
+  // mantissa fit fp16, subnormals included)
+  static __device__ __forceinline__ uint32_t fp8x2(uint32_t w, bool hi) {
+    const f32x2 f = hi ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true)
+                       : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    return pack2(f[0], f[1]);
   }
 };
 

@@ -9,23 +9,40 @@ namespace pal {
 
 constexpr int kF16 = 0;   // == PAL_DTYPE_FLOAT16
 constexpr int kBF16 = 1;  // == PAL_DTYPE_BFLOAT16
+constexpr int kFP8 = 2;   // == PAL_DTYPE_FP8_E4M3 (pools only)
+constexpr int kF32 = 3;   // == PAL_DTYPE_FLOAT32 (fill sources only)
 
-// fill_kv_pages: scatter of new K/V rows into the paged pools.
+constexpr int kMaxFillHeadDim = 256;
+
+// fill_kv_pages: scatter of new K/V rows into the paged pools, optionally
+// with RoPE on K (and Q) and a cast from fp32 / 16-bit to the pool dtype.
 struct FillParams {
-  const uint16_t* new_k;       // [N, Hkv, HD]
-  const uint16_t* new_v;       // [N, Hkv, HD]
-  uint16_t* k_pool;            // [P, Hkv, HD/8, TPP, 8]
-  uint16_t* v_pool;            // [P, Hkv, HD, TPP]
+  const void* new_k;           // [N, Hkv, HD] src_dtype
+  const void* new_v;           // [N, Hkv, HD] src_dtype
+  void* k_pool;                // [P, Hkv, HD/x, TPP, x], x = 16 / element bytes
+  void* v_pool;                // [P, Hkv, HD, TPP]
+  const float* k_scales;       // fp8 pools: [P, Hkv] dequantisation scales
+  const float* v_scales;
   const uint32_t* page_table;  // [S, W]
   const int32_t* write_pos;    // [N]
   const uint32_t* q2seq;       // [N]
+  const float* cos_sin;        // rope: [cos_sin_rows, rotary_dim] (cos | sin)
+  const void* q_in;            // rope, optional: [N, Hq, HD] src_dtype
+  void* q_out;                 // [N, Hq, HD] q_out_dtype (16-bit)
   int64_t num_tokens;
   int64_t num_pages;
   int64_t num_seqs;
   int64_t page_table_width;
+  int64_t cos_sin_rows;
   int num_kv_heads;
+  int num_q_heads;
   int head_dim;
   int tokens_per_page;
+  int src_dtype;               // kF16, kBF16, kF32
+  int kv_dtype;                // kF16, kBF16, kFP8
+  int q_out_dtype;             // kF16, kBF16
+  int rope_style;              // 0 none, 1 NeoX (rotate halves), 2 GPT-J (rotate pairs)
+  int rotary_dim;
 };
 
 hipError_t launch_fill_kv_pages(const FillParams& p, hipStream_t stream);
@@ -36,8 +53,10 @@ hipError_t launch_fill_kv_pages(const FillParams& p, hipStream_t stream);
 // segments that several virtual workers shared.
 struct DecodeParams {
   const uint16_t* q;           // [>=S, Hq, HD]
-  const uint16_t* k_pool;      // [P, Hkv, HD/8, TPP, 8]
-  const uint16_t* v_pool;      // [P, Hkv, HD, TPP]
+  const void* k_pool;          // [P, Hkv, HD/x, TPP, x]: 16-bit (x = 8) or fp8 (x = 16)
+  const void* v_pool;          // [P, Hkv, HD, TPP]
+  const float* k_scales;       // fp8 pools: [P, Hkv] (null: 16-bit pools of the query dtype)
+  const float* v_scales;
   const uint32_t* page_table;  // [S, W]
   const int32_t* seq_lens;     // [S]
   uint16_t* out;               // [S, Hq, HD] (row mode: [R, Hq, HD])
@@ -73,9 +92,9 @@ struct DecodeParams {
 
 // Workers the GPU keeps resident for this kernel configuration (shared_cu:
 // the fused op's decode, one workgroup per CU beside the prefill tiles;
-// chunks: the fixed-chunk mode, partition_size > 0).
+// chunks: the fixed-chunk mode, partition_size > 0; kv8: fp8 pools).
 hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, bool chunks,
-                                   int* workers);
+                                   bool kv8, int* workers);
 // Virtual workers (merge-list and partial slots) a call can produce: the
 // resident workers' equal shares, or, with a partition size, one per fixed
 // chunk of max_blocks (the 16-token blocks the page tables can hold).

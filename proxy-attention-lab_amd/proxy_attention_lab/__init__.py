@@ -11,11 +11,14 @@ from proxy_attention_lab.layout import (
     get_optimal_page_size,
     get_v_cache_shape,
 )
+from proxy_attention_lab.layout import FP8_DTYPE
 from proxy_attention_lab.ops import (
     fill_kv_pages,
     paged_attention,
     paged_attention_decode,
     paged_attention_prefill,
+    rope_cos_sin_cache,
+    rope_fill_kv_pages,
 )
 
 __version__ = "2025.06.4+gfx950"
@@ -29,4 +32,7 @@ __all__ = [
     "paged_attention",
     "paged_attention_decode",
     "paged_attention_prefill",
+    "rope_cos_sin_cache",
+    "rope_fill_kv_pages",
+    "FP8_DTYPE",
 ]

@@ -23,6 +23,12 @@ PAL_ERR_HIP = -3
 
 DTYPE_FLOAT16 = 0
 DTYPE_BFLOAT16 = 1
+DTYPE_FP8_E4M3 = 2
+DTYPE_FLOAT32 = 3
+
+ROPE_NONE = 0
+ROPE_NEOX = 1
+ROPE_GPTJ = 2
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -41,6 +47,17 @@ _SIGNATURES = {
         _c_int,
         [_c_void_p] * 7 + [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_void_p],
     ),
+    "pal_fill_kv_pages_fp8": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int] + [_c_void_p] * 7
+        + [_c_i64, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_void_p],
+    ),
+    "pal_rope_fill_kv_pages": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int] + [_c_void_p] * 5
+        + [_c_i64, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64]
+        + [_c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p],
+    ),
     "pal_paged_attention_decode_workspace_size": (
         _c_size_t,
         [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int],
@@ -48,6 +65,16 @@ _SIGNATURES = {
     "pal_paged_attention_decode": (
         _c_int,
         [_c_void_p] * 6
+        + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int]
+        + [_c_void_p, _c_size_t, _c_void_p],
+    ),
+    "pal_paged_attention_decode_fp8_workspace_size": (
+        _c_size_t,
+        [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int],
+    ),
+    "pal_paged_attention_decode_fp8": (
+        _c_int,
+        [_c_void_p] * 8
         + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int]
         + [_c_void_p, _c_size_t, _c_void_p],
     ),

@@ -24,11 +24,19 @@ import contextlib
 import torch
 
 from . import _lib
-from .layout import dtype_code, get_k_cache_stripe_size  # noqa: F401  (re-exported)
+from .layout import (  # noqa: F401  (get_k_cache_stripe_size re-exported)
+    FP8_DTYPE,
+    dtype_code,
+    get_k_cache_stripe_size,
+    pool_dtype_code,
+    source_dtype_code,
+)
 
 __all__ = [
     "fill_kv_pages",
     "get_k_cache_stripe_size",
+    "rope_cos_sin_cache",
+    "rope_fill_kv_pages",
     "paged_attention",
     "paged_attention_decode",
     "paged_attention_prefill",
@@ -116,7 +124,8 @@ def _workspace(kind: str, nbytes: int, device: torch.device, stream_handle: int)
 
 
 def _pools(op: str, k_pool: torch.Tensor, v_pool: torch.Tensor, device: torch.device, dtype: torch.dtype):
-    """Validate the paged pools; return (num_pages, Hkv, HD, TPP)."""
+    """Validate the paged pools; return (num_pages, Hkv, HD, TPP).  Pools hold
+    the query dtype, or fp8 e4m3 (torch.float8_e4m3fn, K stripe of 16)."""
     for name, t in (("k_cache_pool", k_pool), ("v_cache_pool", v_pool)):
         _require_device(name, t, device)
     if v_pool.dim() != 4:
@@ -124,12 +133,30 @@ def _pools(op: str, k_pool: torch.Tensor, v_pool: torch.Tensor, device: torch.de
     if k_pool.dim() != 5:
         raise ValueError(f"[{op}] k_cache_pool must be 5D [pages, kv_heads, head_dim/x, tokens_per_page, x]")
     num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in v_pool.shape)
-    if k_pool.dtype != dtype or v_pool.dtype != dtype:
-        raise ValueError(f"[{op}] queries and pools must share one dtype")
-    expect_k = (num_pages, num_kv_heads, head_dim // 8, tpp, 8)
+    if k_pool.dtype != v_pool.dtype or k_pool.dtype not in (dtype, FP8_DTYPE):
+        raise ValueError(f"[{op}] pools must share one dtype: the queries' or float8_e4m3fn")
+    x = get_k_cache_stripe_size(k_pool.dtype)
+    expect_k = (num_pages, num_kv_heads, head_dim // x, tpp, x)
     if tuple(k_pool.shape) != expect_k:
         raise ValueError(f"[{op}] k_cache_pool shape {tuple(k_pool.shape)} != {expect_k}")
     return num_pages, num_kv_heads, head_dim, tpp
+
+
+def _scales(op: str, k_pool: torch.Tensor, k_scales, v_scales, num_pages: int, num_kv_heads: int,
+            device: torch.device):
+    """(k_scales, v_scales) for fp8 pools (validated), (None, None) for
+    16-bit pools (where giving scales is an error)."""
+    if k_pool.dtype != FP8_DTYPE:
+        if k_scales is not None or v_scales is not None:
+            raise ValueError(f"[{op}] k_scales / v_scales apply to fp8 pools only")
+        return None, None
+    for name, t in (("k_scales", k_scales), ("v_scales", v_scales)):
+        if t is None:
+            raise ValueError(f"[{op}] fp8 pools need k_scales and v_scales ([num_pages, num_kv_heads] float32)")
+        _require_device(name, t, device)
+        if t.dtype != torch.float32 or tuple(t.shape) != (num_pages, num_kv_heads):
+            raise ValueError(f"[{op}] {name} must be float32 [{num_pages}, {num_kv_heads}]")
+    return k_scales, v_scales
 
 
 def _query_dims(op: str, queries: torch.Tensor, head_dim: int):
@@ -160,6 +187,8 @@ def paged_attention_decode(
     stream=None,
     *,
     partition_size: int = 0,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Decode attention: one query row per sequence over its paged context.
 
@@ -177,7 +206,10 @@ def paged_attention_decode(
     or 512 splits the KV stream into fixed chunks of that many tokens instead
     (each worker streams an equal run of consecutive chunks, every chunk its
     own partial); partials are merged by log-sum-exp as in the reference's
-    two-pass mode.
+    two-pass mode.  fp8 pools (torch.float8_e4m3fn, an addition) need
+    ``k_scales`` / ``v_scales`` (float32 [num_pages, Hkv]): a key or value
+    is its code times the scale of its (page, kv head); head_dim 64, 128 or
+    256.
     """
     op = "paged_attention_decode"
     _require_device("queries", queries)
@@ -185,6 +217,7 @@ def paged_attention_decode(
     code = dtype_code(queries.dtype)
     num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_pool, v_cache_pool, device, queries.dtype)
     num_rows, num_q_heads = _query_dims(op, queries, head_dim)
+    ks, vs = _scales(op, k_cache_pool, k_scales, v_scales, num_pages, num_kv_heads, device)
     if page_table.dim() != 2:
         raise ValueError("[paged_attention_decode] page_table must be 2D [num_seqs, max_pages_per_seq]")
     num_seqs, width = (int(x) for x in page_table.shape)
@@ -202,19 +235,77 @@ def paged_attention_decode(
         vp = v_cache_pool.contiguous()
         out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=queries.dtype, device=device)
         ws = None
+        fp8 = ks is not None
         if num_seqs > 0:
+            size_fn = L.pal_paged_attention_decode_fp8_workspace_size if fp8 else \
+                L.pal_paged_attention_decode_workspace_size
             with torch.cuda.device(device):
-                ws_bytes = L.pal_paged_attention_decode_workspace_size(
-                    code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width, int(partition_size))
+                ws_bytes = size_fn(code, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, width,
+                                   int(partition_size))
             ws = _workspace("decode", ws_bytes, device, sh)
-        status = L.pal_paged_attention_decode(
-            _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
-            code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
-            num_pages, width, int(partition_size),
-            _ptr(ws), ws.numel() if ws is not None else 0, sh,
-        )
+        if fp8:
+            status = L.pal_paged_attention_decode_fp8(
+                _ptr(q), _ptr(kp), _ptr(vp), _ptr(ks.contiguous()), _ptr(vs.contiguous()), _ptr(pt), _ptr(lens),
+                _ptr(out), code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width,
+                int(partition_size), _ptr(ws), ws.numel() if ws is not None else 0, sh)
+        else:
+            status = L.pal_paged_attention_decode(
+                _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(out),
+                code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
+                num_pages, width, int(partition_size),
+                _ptr(ws), ws.numel() if ws is not None else 0, sh,
+            )
     _lib.check(status)
     return out
+
+
+def _fill_common(op: str, new_keys, new_values, k_pool, v_pool, page_table, write_positions, query_to_seq_map,
+                 k_scales, v_scales):
+    """Validation shared by fill_kv_pages and rope_fill_kv_pages; returns
+    (device, num_tokens, num_pages, Hkv, HD, TPP, width, num_seqs, pool code,
+    source code)."""
+    # ops.cpp:204-211: the same rank checks, first, raised as ValueError.
+    if k_pool.dim() != 5:
+        raise ValueError(f"[{op}] global_key_pool must be 5D.")
+    if v_pool.dim() != 4:
+        raise ValueError(f"[{op}] global_value_pool must be 4D.")
+    _require_device("new_keys", new_keys)
+    device = new_keys.device
+    for name, t in (("new_values", new_values), ("global_key_pool", k_pool), ("global_value_pool", v_pool)):
+        _require_device(name, t, device)
+    num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in v_pool.shape)
+    pool_code = pool_dtype_code(k_pool.dtype)
+    if v_pool.dtype != k_pool.dtype:
+        raise ValueError(f"[{op}] key and value pools must share one dtype")
+    src_code = source_dtype_code(new_keys.dtype)
+    if new_values.dtype != new_keys.dtype:
+        raise ValueError(f"[{op}] new keys and values must share one dtype")
+    x = get_k_cache_stripe_size(k_pool.dtype)
+    expect_k = (num_pages, num_kv_heads, head_dim // x, tpp, x)
+    if tuple(k_pool.shape) != expect_k:
+        raise ValueError(f"[{op}] global_key_pool shape {tuple(k_pool.shape)} != {expect_k}")
+    if not k_pool.is_contiguous() or not v_pool.is_contiguous():
+        raise ValueError(f"[{op}] pools must be contiguous (they are updated in place)")
+    if pool_code == _lib.DTYPE_FP8_E4M3:
+        for name, t in (("k_scales", k_scales), ("v_scales", v_scales)):
+            if t is None:
+                raise ValueError(f"[{op}] fp8 pools need k_scales and v_scales ([num_pages, num_kv_heads] float32)")
+            _require_device(name, t, device)
+            if t.dtype != torch.float32 or tuple(t.shape) != (num_pages, num_kv_heads) or not t.is_contiguous():
+                raise ValueError(f"[{op}] {name} must be contiguous float32 [{num_pages}, {num_kv_heads}]")
+    n = int(new_keys.shape[0]) if new_keys.dim() > 0 else 0
+    if n and (tuple(new_keys.shape) != (n, num_kv_heads, head_dim) or
+              tuple(new_values.shape) != (n, num_kv_heads, head_dim)):
+        raise ValueError(
+            f"[{op}] new_keys/new_values must be [{n}, {num_kv_heads}, {head_dim}], got "
+            f"{tuple(new_keys.shape)} / {tuple(new_values.shape)}"
+        )
+    if page_table.dim() != 2:
+        raise ValueError(f"[{op}] page_table must be 2D")
+    num_seqs, width = (int(x) for x in page_table.shape)
+    if write_positions.numel() < n or query_to_seq_map.numel() < n:
+        raise ValueError(f"[{op}] write positions and query_to_seq_map need one entry per new token")
+    return device, n, num_pages, num_kv_heads, head_dim, tpp, width, num_seqs, pool_code, src_code
 
 
 def fill_kv_pages(
@@ -228,8 +319,10 @@ def fill_kv_pages(
     stream=None,
     *,
     copy: bool = False,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Scatter new K/V rows into their page slots (bit-exact copy).
+    """Scatter new K/V rows into their page slots.
 
     Reference: ops.py:133-171 -> bindings.cpp:182-222 -> ops.cpp:188-239 ->
     fill_kv_pages_primitive.cpp:70-170 -> fill_kv_pages.h.metal:56-116.
@@ -237,30 +330,20 @@ def fill_kv_pages(
     new_keys / new_values: [N, Hkv, HD]; pools as for decode;
     current_token_write_positions: [N] int32; query_to_seq_map: [N] uint32.
     Token t goes to page page_table[q2seq[t], pos // TPP], slot pos % TPP.
+    With new rows in the pool dtype this is a bit-exact copy, as in the
+    reference.  Additions: float32 rows (or 16-bit rows of the other
+    dtype) are cast to the pool dtype (round to nearest even), and fp8 pools
+    (torch.float8_e4m3fn, K stripe of 16) are written quantized with the
+    keyword-only ``k_scales`` / ``v_scales`` (float32 [num_pages, Hkv]):
+    q = x / scale held to [-448, 448], rounded to nearest even.
     Updates the pools in place and returns them; with ``copy=True`` the
     inputs are left untouched and fresh pools are returned, as in the
     reference.
     """
-    # ops.cpp:204-211: the same rank checks, first, raised as ValueError.
-    if global_key_pool.dim() != 5:
-        raise ValueError("[fill_kv_pages] global_key_pool must be 5D.")
-    if global_value_pool.dim() != 4:
-        raise ValueError("[fill_kv_pages] global_value_pool must be 4D.")
-    _require_device("new_keys", new_keys)
-    device = new_keys.device
-    for name, t in (("new_values", new_values), ("global_key_pool", global_key_pool),
-                    ("global_value_pool", global_value_pool)):
-        _require_device(name, t, device)
-    num_pages, num_kv_heads, head_dim, tpp = (int(x) for x in global_value_pool.shape)
-    code = dtype_code(global_key_pool.dtype)
-    if not (new_keys.dtype == new_values.dtype == global_key_pool.dtype == global_value_pool.dtype):
-        raise ValueError("[fill_kv_pages] new keys/values and pools must share one dtype")
-    expect_k = (num_pages, num_kv_heads, head_dim // 8, tpp, 8)
-    if tuple(global_key_pool.shape) != expect_k:
-        raise ValueError(f"[fill_kv_pages] global_key_pool shape {tuple(global_key_pool.shape)} != {expect_k}")
-    if not global_key_pool.is_contiguous() or not global_value_pool.is_contiguous():
-        raise ValueError("[fill_kv_pages] pools must be contiguous (they are updated in place)")
-    n = int(new_keys.shape[0]) if new_keys.dim() > 0 else 0
+    op = "fill_kv_pages"
+    device, n, num_pages, hkv, hd, tpp, width, num_seqs, pool_code, src_code = _fill_common(
+        op, new_keys, new_values, global_key_pool, global_value_pool, page_table, current_token_write_positions,
+        query_to_seq_map, k_scales, v_scales)
     sh = _stream_handle(stream, device)
     if copy:
         with _on_stream(sh, device):
@@ -268,28 +351,130 @@ def fill_kv_pages(
             global_value_pool = global_value_pool.clone()
     if n == 0 or new_keys.numel() == 0:
         return global_key_pool, global_value_pool
-    if tuple(new_keys.shape) != (n, num_kv_heads, head_dim) or tuple(new_values.shape) != (n, num_kv_heads, head_dim):
-        raise ValueError(
-            f"[fill_kv_pages] new_keys/new_values must be [{n}, {num_kv_heads}, {head_dim}], got "
-            f"{tuple(new_keys.shape)} / {tuple(new_values.shape)}"
-        )
-    if page_table.dim() != 2:
-        raise ValueError("[fill_kv_pages] page_table must be 2D")
-    num_seqs, width = (int(x) for x in page_table.shape)
-    if current_token_write_positions.numel() < n or query_to_seq_map.numel() < n:
-        raise ValueError("[fill_kv_pages] write positions and query_to_seq_map need one entry per new token")
+    L = _lib.lib()
     with _on_stream(sh, device):
         pt = _index_tensor("page_table", page_table, device)
         pos = _index_tensor("current_token_write_positions", current_token_write_positions, device)
         q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
         nk = new_keys.contiguous()
         nv = new_values.contiguous()
-        status = _lib.lib().pal_fill_kv_pages(
-            _ptr(nk), _ptr(nv), _ptr(global_key_pool), _ptr(global_value_pool), _ptr(pt), _ptr(pos), _ptr(q2s),
-            code, n, num_kv_heads, head_dim, tpp, num_pages, num_seqs, width, sh,
-        )
+        if pool_code == _lib.DTYPE_FP8_E4M3:
+            status = L.pal_fill_kv_pages_fp8(
+                _ptr(nk), _ptr(nv), src_code, _ptr(global_key_pool), _ptr(global_value_pool), _ptr(k_scales),
+                _ptr(v_scales), _ptr(pt), _ptr(pos), _ptr(q2s), n, hkv, hd, tpp, num_pages, num_seqs, width, sh)
+        elif src_code == pool_code:
+            status = L.pal_fill_kv_pages(
+                _ptr(nk), _ptr(nv), _ptr(global_key_pool), _ptr(global_value_pool), _ptr(pt), _ptr(pos), _ptr(q2s),
+                pool_code, n, hkv, hd, tpp, num_pages, num_seqs, width, sh)
+        else:  # a cast on the way: the fused entry without rotation
+            status = L.pal_rope_fill_kv_pages(
+                _ptr(nk), _ptr(nv), src_code, _ptr(global_key_pool), _ptr(global_value_pool), pool_code, None, None,
+                _ptr(pt), _ptr(pos), _ptr(q2s), n, hkv, hd, tpp, num_pages, num_seqs, width, None, 0, 0,
+                _lib.ROPE_NONE, None, None, 0, _lib.DTYPE_BFLOAT16, sh)
     _lib.check(status)
     return global_key_pool, global_value_pool
+
+
+_ROPE_STYLES = {"neox": _lib.ROPE_NEOX, "gptj": _lib.ROPE_GPTJ}
+_COS_SIN: dict[tuple, torch.Tensor] = {}
+
+
+def rope_cos_sin_cache(max_position: int, rotary_dim: int, base: float = 10000.0,
+                       device: torch.device | str = "cuda") -> torch.Tensor:
+    """The cos/sin table rope_fill_kv_pages reads: [max_position, rotary_dim]
+    float32, cos(p w_f) for the rotary_dim / 2 frequencies w_f =
+    base^(-2f / rotary_dim), then sin(p w_f), computed in float64 and rounded
+    once.  Cached per (arguments, device)."""
+    device = torch.device(device)
+    key = (int(max_position), int(rotary_dim), float(base), str(device))
+    t = _COS_SIN.get(key)
+    if t is None:
+        half = rotary_dim // 2
+        inv_freq = float(base) ** (-(2.0 * torch.arange(half, dtype=torch.float64)) / rotary_dim)
+        ang = torch.arange(max_position, dtype=torch.float64)[:, None] * inv_freq[None, :]
+        t = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).to(device)
+        _COS_SIN[key] = t
+    return t
+
+
+def rope_fill_kv_pages(
+    new_keys: torch.Tensor,
+    new_values: torch.Tensor,
+    global_key_pool: torch.Tensor,
+    global_value_pool: torch.Tensor,
+    page_table: torch.Tensor,
+    current_token_write_positions: torch.Tensor,
+    query_to_seq_map: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    stream=None,
+    *,
+    queries: torch.Tensor | None = None,
+    rotary_dim: int | None = None,
+    style: str = "neox",
+    query_dtype: torch.dtype | None = None,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """RoPE + cast + KV scatter in one pass: the step that produces
+    fill_kv_pages' inputs from the QKV projection, fused with it (no
+    reference counterpart; the scatter is fill_kv_pages', ops.py:133-171).
+
+    new_keys / new_values: [N, Hkv, HD] float32, float16 or bfloat16 (the
+    projection's output); the position of token t is
+    current_token_write_positions[t].  K is rotated by row `pos` of
+    ``cos_sin_cache`` ([rows, rotary_dim] float32, see rope_cos_sin_cache):
+    style "neox" pairs dims (f, f + rotary_dim/2), "gptj" pairs (2f, 2f+1);
+    dims past rotary_dim (default: the whole head) pass through.  K and V
+    are then cast to the pool dtype (fp8 pools: with ``k_scales`` /
+    ``v_scales``) and scattered like fill_kv_pages, in place.  ``queries``
+    ([N, Hq, HD], same dtype as new_keys), if given, are rotated the same way
+    and returned cast to ``query_dtype`` (default: the pool dtype, or
+    bfloat16 for fp8 pools).  Tokens whose position has no row in the table
+    are not written to the pools; their queries are cast unrotated.
+    Returns (key_pool, value_pool, rotated queries or None).
+    """
+    op = "rope_fill_kv_pages"
+    device, n, num_pages, hkv, hd, tpp, width, num_seqs, pool_code, src_code = _fill_common(
+        op, new_keys, new_values, global_key_pool, global_value_pool, page_table, current_token_write_positions,
+        query_to_seq_map, k_scales, v_scales)
+    if style not in _ROPE_STYLES:
+        raise ValueError(f"[{op}] style must be 'neox' or 'gptj', got {style!r}")
+    rot = hd if rotary_dim is None else int(rotary_dim)
+    _require_device("cos_sin_cache", cos_sin_cache, device)
+    if cos_sin_cache.dim() != 2 or int(cos_sin_cache.shape[1]) != rot or cos_sin_cache.dtype != torch.float32:
+        raise ValueError(f"[{op}] cos_sin_cache must be float32 [rows, {rot}]")
+    q_out = None
+    hq = 0
+    if queries is not None:
+        _require_device("queries", queries, device)
+        if queries.dtype != new_keys.dtype or queries.dim() != 3 or int(queries.shape[0]) != n or \
+                int(queries.shape[2]) != hd:
+            raise ValueError(f"[{op}] queries must be [{n}, Hq, {hd}] in the dtype of new_keys")
+        hq = int(queries.shape[1])
+        if query_dtype is None:
+            query_dtype = global_key_pool.dtype if pool_code != _lib.DTYPE_FP8_E4M3 else torch.bfloat16
+        q_code = dtype_code(query_dtype)
+    else:
+        q_code = _lib.DTYPE_BFLOAT16
+    sh = _stream_handle(stream, device)
+    with _on_stream(sh, device):
+        if queries is not None:
+            q_out = torch.empty((n, hq, hd), dtype=query_dtype, device=device)
+        if n == 0:
+            return global_key_pool, global_value_pool, q_out
+        pt = _index_tensor("page_table", page_table, device)
+        pos = _index_tensor("current_token_write_positions", current_token_write_positions, device)
+        q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
+        nk = new_keys.contiguous()
+        nv = new_values.contiguous()
+        cs = cos_sin_cache.contiguous()
+        qi = queries.contiguous() if queries is not None else None
+        status = _lib.lib().pal_rope_fill_kv_pages(
+            _ptr(nk), _ptr(nv), src_code, _ptr(global_key_pool), _ptr(global_value_pool), pool_code,
+            _ptr(k_scales), _ptr(v_scales), _ptr(pt), _ptr(pos), _ptr(q2s), n, hkv, hd, tpp, num_pages, num_seqs,
+            width, _ptr(cs), int(cs.shape[0]), rot, _ROPE_STYLES[style], _ptr(qi), _ptr(q_out), hq, q_code, sh)
+    _lib.check(status)
+    return global_key_pool, global_value_pool, q_out
 
 
 def paged_attention_prefill(
@@ -321,6 +506,8 @@ def paged_attention_prefill(
     device = q_prompt.device
     code = dtype_code(q_prompt.dtype)
     num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_paged, v_cache_paged, device, q_prompt.dtype)
+    if k_cache_paged.dtype == FP8_DTYPE:
+        raise ValueError(f"[{op}] fp8 pools are not supported by this operator")
     num_rows, num_q_heads = _query_dims(op, q_prompt, head_dim)
     for name, t in (("k_prompt", k_prompt), ("v_prompt", v_prompt)):
         _require_device(name, t, device)
@@ -383,6 +570,8 @@ def paged_attention(
     device = queries.device
     code = dtype_code(queries.dtype)
     num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_pool, v_cache_pool, device, queries.dtype)
+    if k_cache_pool.dtype == FP8_DTYPE:
+        raise ValueError(f"[{op}] fp8 pools are not supported by this operator")
     num_rows, num_q_heads = _query_dims(op, queries, head_dim)
     if page_table.dim() != 2:
         raise ValueError(f"[{op}] page_table must be 2D [num_seqs, max_pages_per_seq]")
