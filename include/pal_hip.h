@@ -238,6 +238,21 @@ int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, cons
                                 int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* stream);
 
 /*
+ * paged_attention_prefill over fp8 e4m3 paged history (no reference
+ * counterpart; semantics of pal_paged_attention_prefill, ops.py:87-130):
+ * the history's keys and values are their codes times the (page, kv head)
+ * scales (k_scales / v_scales, fp32 [num_pages, Hkv]), dequantized to dtype
+ * on the way into the tile; the dense prompt K/V and the queries are in
+ * dtype.  head_dim 64, 128 or 256.
+ */
+int pal_paged_attention_prefill_fp8(const void* q_prompt, const void* k_prompt, const void* v_prompt,
+                                    const void* k_cache_paged, const void* v_cache_paged, const float* k_scales,
+                                    const float* v_scales, const uint32_t* page_table, const int32_t* context_lens,
+                                    void* out, int dtype, int64_t num_query_rows, int64_t num_seqs, int num_q_heads,
+                                    int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                                    int64_t page_table_width, void* stream);
+
+/*
  * Workspace bytes pal_paged_attention needs for num_query_rows rows on the
  * current device (0 for unsupported arguments or without a device).  Zero-fill
  * it before its first use; each call leaves it ready for the next one.
@@ -269,6 +284,22 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
                         int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page,
                         int64_t num_pages, int64_t page_table_width, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/*
+ * The fused mixed batch over fp8 e4m3 pools (pal_paged_attention's
+ * semantics; keys and values are codes times their (page, kv head) scale,
+ * k_scales / v_scales fp32 [num_pages, Hkv]).  No reference counterpart.
+ * head_dim 64, 128 or 256; workspace from
+ * pal_paged_attention_fp8_workspace_size.
+ */
+size_t pal_paged_attention_fp8_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, int num_kv_heads,
+                                              int head_dim, int tokens_per_page);
+int pal_paged_attention_fp8(const void* queries, const void* k_pool, const void* v_pool, const float* k_scales,
+                            const float* v_scales, const uint32_t* page_table, const int32_t* sequence_lengths,
+                            const uint32_t* query_to_seq_map, const int32_t* query_token_offset, void* out, int dtype,
+                            int64_t num_query_rows, int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                            int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -307,6 +307,197 @@ int fill_call(const char* op, const FillArgs& a, hipStream_t stream) {
   return hip_status(pal::launch_fill_kv_pages(p, stream), op);
 }
 
+// fp8 pools: both scale arrays, and a head dim of whole 64-dim rounds
+int check_fp8_scales(const char* op, const float* k_scales, const float* v_scales, int head_dim) {
+  if (!k_scales && !v_scales) return PAL_OK;
+  if (!k_scales || !v_scales) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] fp8 pools need both k_scales and v_scales", op);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PAL_ERR_RUNTIME, "[%s] no fp8 kernel for head_dim %d (supported: 64, 128, 256)", op, head_dim);
+  return PAL_OK;
+}
+
+int prefill_call(const void* q_prompt, const void* k_prompt, const void* v_prompt, const void* k_cache_paged,
+                 const void* v_cache_paged, const float* k_scales, const float* v_scales, const uint32_t* page_table,
+                 const int32_t* context_lens, void* out, int dtype, int64_t num_query_rows, int64_t num_seqs,
+                 int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                 int64_t page_table_width, hipStream_t stream) {
+  const char* op = "paged_attention_prefill";
+  int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                                page_table_width);
+  if (st != PAL_OK) return st;
+  st = check_fp8_scales(op, k_scales, v_scales, head_dim);
+  if (st != PAL_OK) return st;
+  if (num_query_rows < 0 || num_seqs < 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative dimension", op);
+  if (head_dim % 32 != 0)
+    return fail(PAL_ERR_RUNTIME, "[%s] head_dim %d must be divisible by 32", op, head_dim);
+  if (!prefill_head_dim_supported(head_dim))
+    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for head_dim %d (supported: 32, 64, 96, 128, 256)", op, head_dim);
+  if (num_seqs == 0) return ok();
+  if (num_pages == 0) page_table_width = 0;  // no page to read: no history
+  const int64_t prompt_len = num_query_rows / num_seqs;
+  if (prompt_len == 0) return ok();
+  if (!q_prompt || !k_prompt || !v_prompt || !context_lens || !out ||
+      (num_pages > 0 && (!k_cache_paged || !v_cache_paged)) || (page_table_width > 0 && !page_table))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
+  if (!aligned16(q_prompt) || !aligned16(k_prompt) || !aligned16(v_prompt) || !aligned16(k_cache_paged) ||
+      !aligned16(v_cache_paged) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] inputs must be 16-byte aligned, out 8-byte aligned", op);
+  const int group = num_q_heads / num_kv_heads;
+  const int hg_max = group < 16 ? group : 16;
+  const int qt = pal::prefill_tokens_per_tile(group);
+  const int64_t tiles = num_seqs * ((prompt_len + qt - 1) / qt);
+  if (tiles * num_kv_heads * ((group + 15) / 16) > 0x7fffffffLL || num_query_rows > 0x7fffffffLL)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
+  pal::PrefillParams p;
+  p.q = static_cast<const uint16_t*>(q_prompt);
+  p.out = static_cast<uint16_t*>(out);
+  p.k_pool = static_cast<const uint16_t*>(k_cache_paged);
+  p.v_pool = static_cast<const uint16_t*>(v_cache_paged);
+  p.k_scales = k_scales;
+  p.v_scales = v_scales;
+  p.k_dense = static_cast<const uint16_t*>(k_prompt);
+  p.v_dense = static_cast<const uint16_t*>(v_prompt);
+  p.page_table = page_table;
+  p.seq_lens = context_lens;
+  p.q_offset = nullptr;
+  p.q2seq = nullptr;
+  p.num_rows = num_query_rows;
+  p.num_seqs = num_seqs;
+  p.num_pages = num_pages;
+  p.page_table_width = page_table_width;
+  p.num_units = static_cast<int>(tiles);
+  p.prompt_len = static_cast<int>(prompt_len);
+  p.num_q_heads = num_q_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = group;
+  p.head_chunks = (group + 15) / 16;
+  p.hg_max = hg_max;
+  p.scale_log2 = scale_log2_for(head_dim);
+  p.scale_inv_log2 = 1.f / p.scale_log2;
+  return hip_status(pal::launch_prefill(p, dtype, head_dim, tokens_per_page, stream), op);
+}
+
+size_t fused_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, int num_kv_heads, int head_dim,
+                            int tokens_per_page, bool kv8) {
+  if (!valid_dtype(dtype) || num_query_rows <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0 || !prefill_head_dim_supported(head_dim) ||
+      (tokens_per_page != 16 && tokens_per_page != 32) || num_query_rows > 0x7fffffffLL)
+    return 0;
+  if (kv8 && head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
+  const int group = num_q_heads / num_kv_heads;
+  int resident = 0;
+  int64_t vw = 0;
+  if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
+                     true, kv8, &resident, &vw) != PAL_OK)
+    return 0;
+  return decode_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
+}
+
+int fused_call(const void* queries, const void* k_pool, const void* v_pool, const float* k_scales,
+               const float* v_scales, const uint32_t* page_table, const int32_t* sequence_lengths,
+               const uint32_t* query_to_seq_map, const int32_t* query_token_offset, void* out, int dtype,
+               int64_t num_query_rows, int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+               int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* workspace,
+               size_t workspace_bytes, hipStream_t hs) {
+  const char* op = "paged_attention";
+  int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
+                                page_table_width);
+  if (st != PAL_OK) return st;
+  st = check_fp8_scales(op, k_scales, v_scales, head_dim);
+  if (st != PAL_OK) return st;
+  const bool kv8 = k_scales != nullptr;
+  if (num_query_rows < 0 || num_seqs < 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative dimension", op);
+  if (!prefill_head_dim_supported(head_dim))
+    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for head_dim %d (supported: 32, 64, 96, 128, 256)", op, head_dim);
+  if (num_query_rows > 0x7fffffffLL || num_seqs > 0x7fffffffLL)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
+  if (num_query_rows == 0) return ok();
+  if (num_pages == 0) page_table_width = 0;  // no page to read: every row is empty
+  if (!queries || !sequence_lengths || !query_to_seq_map || !query_token_offset || !out ||
+      (num_pages > 0 && (!k_pool || !v_pool)) || (page_table_width > 0 && !page_table))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
+  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] queries and pools must be 16-byte aligned, out 8-byte aligned", op);
+  const int group = num_q_heads / num_kv_heads;
+  const int hg_max = group < 16 ? group : 16;
+  const int chunks = (group + 15) / 16;
+  int resident = 0;
+  int64_t vw = 0;
+  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, true, kv8,
+                      &resident,
+                      &vw);
+  if (st != PAL_OK) return st;
+  const DecodeLayout lay = decode_layout(num_query_rows, head_dim, hg_max, vw);
+  if (workspace == nullptr || workspace_bytes < lay.total)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace of %zu bytes needed, %zu given", op, lay.total,
+                workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace must be 256-byte aligned", op);
+  const int qt = pal::prefill_tokens_per_tile(group);
+  const int64_t windows = (num_query_rows + qt - 1) / qt;
+  if (windows * num_kv_heads * chunks > 0x7fffffffLL)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
+
+  // 1. runs of rows of one sequence: MFMA tiles over windows of rows
+  pal::PrefillParams pp;
+  pp.q = static_cast<const uint16_t*>(queries);
+  pp.out = static_cast<uint16_t*>(out);
+  pp.k_pool = static_cast<const uint16_t*>(k_pool);
+  pp.v_pool = static_cast<const uint16_t*>(v_pool);
+  pp.k_scales = k_scales;
+  pp.v_scales = v_scales;
+  pp.k_dense = nullptr;
+  pp.v_dense = nullptr;
+  pp.page_table = page_table;
+  pp.seq_lens = sequence_lengths;
+  pp.q_offset = query_token_offset;
+  pp.q2seq = query_to_seq_map;
+  pp.num_rows = num_query_rows;
+  pp.num_seqs = num_seqs;
+  pp.num_pages = num_pages;
+  pp.page_table_width = page_table_width;
+  pp.num_units = static_cast<int>(windows);
+  pp.prompt_len = 0;
+  pp.num_q_heads = num_q_heads;
+  pp.num_kv_heads = num_kv_heads;
+  pp.group = group;
+  pp.head_chunks = chunks;
+  pp.hg_max = hg_max;
+  pp.scale_log2 = scale_log2_for(head_dim);
+  pp.scale_inv_log2 = 1.f / pp.scale_log2;
+  // 2. rows alone in their run: split-K decode
+  pal::DecodeParams dp = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
+                                       static_cast<char*>(workspace), lay, num_query_rows, num_pages,
+                                       page_table_width, num_q_heads, num_kv_heads, head_dim, resident, 0);
+  dp.k_scales = k_scales;
+  dp.v_scales = v_scales;
+  dp.q2seq = query_to_seq_map;
+  dp.q_offset = query_token_offset;
+  dp.num_pt_rows = num_seqs;
+
+  // The decode grid (one persistent workgroup per CU) is launched first on
+  // the caller's stream, then the prefill tiles on the side stream fill the
+  // remaining slots; the caller's stream waits for both.
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, op);
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream* ss = nullptr;
+  err = side_stream(dev, &ss);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = hipEventRecord(ss->fork, hs);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = hipStreamWaitEvent(ss->stream, ss->fork, 0);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = pal::launch_decode(dp, dtype, head_dim, tokens_per_page, true, hs);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, ss->stream);
+  if (err != hipSuccess) return hip_status(err, op);
+  err = hipEventRecord(ss->join, ss->stream);
+  if (err != hipSuccess) return hip_status(err, op);
+  return hip_status(hipStreamWaitEvent(hs, ss->join, 0), op);
+}
+
 // pal_paged_attention_decode and its no-allocation variant: with
 // use_scratch the workspace is the library's per-device scratch array (no
 // caller buffer, nothing allocated), and calls needing more than it holds
@@ -569,71 +760,32 @@ int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, cons
                                 const int32_t* context_lens, void* out, int dtype, int64_t num_query_rows,
                                 int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                                 int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* stream) {
-  const char* op = "paged_attention_prefill";
-  int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
-                                page_table_width);
-  if (st != PAL_OK) return st;
-  if (num_query_rows < 0 || num_seqs < 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative dimension", op);
-  if (head_dim % 32 != 0)
-    return fail(PAL_ERR_RUNTIME, "[%s] head_dim %d must be divisible by 32", op, head_dim);
-  if (!prefill_head_dim_supported(head_dim))
-    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for head_dim %d (supported: 32, 64, 96, 128, 256)", op, head_dim);
-  if (num_seqs == 0) return ok();
-  if (num_pages == 0) page_table_width = 0;  // no page to read: no history
-  const int64_t prompt_len = num_query_rows / num_seqs;
-  if (prompt_len == 0) return ok();
-  if (!q_prompt || !k_prompt || !v_prompt || !context_lens || !out ||
-      (num_pages > 0 && (!k_cache_paged || !v_cache_paged)) || (page_table_width > 0 && !page_table))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
-  if (!aligned16(q_prompt) || !aligned16(k_prompt) || !aligned16(v_prompt) || !aligned16(k_cache_paged) ||
-      !aligned16(v_cache_paged) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] inputs must be 16-byte aligned, out 8-byte aligned", op);
-  const int group = num_q_heads / num_kv_heads;
-  const int hg_max = group < 16 ? group : 16;
-  const int qt = pal::prefill_tokens_per_tile(group);
-  const int64_t tiles = num_seqs * ((prompt_len + qt - 1) / qt);
-  if (tiles * num_kv_heads * ((group + 15) / 16) > 0x7fffffffLL || num_query_rows > 0x7fffffffLL)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
-  pal::PrefillParams p;
-  p.q = static_cast<const uint16_t*>(q_prompt);
-  p.out = static_cast<uint16_t*>(out);
-  p.k_pool = static_cast<const uint16_t*>(k_cache_paged);
-  p.v_pool = static_cast<const uint16_t*>(v_cache_paged);
-  p.k_dense = static_cast<const uint16_t*>(k_prompt);
-  p.v_dense = static_cast<const uint16_t*>(v_prompt);
-  p.page_table = page_table;
-  p.seq_lens = context_lens;
-  p.q_offset = nullptr;
-  p.q2seq = nullptr;
-  p.num_rows = num_query_rows;
-  p.num_seqs = num_seqs;
-  p.num_pages = num_pages;
-  p.page_table_width = page_table_width;
-  p.num_units = static_cast<int>(tiles);
-  p.prompt_len = static_cast<int>(prompt_len);
-  p.num_q_heads = num_q_heads;
-  p.num_kv_heads = num_kv_heads;
-  p.group = group;
-  p.head_chunks = (group + 15) / 16;
-  p.hg_max = hg_max;
-  p.scale_log2 = scale_log2_for(head_dim);
-  p.scale_inv_log2 = 1.f / p.scale_log2;
-  return hip_status(pal::launch_prefill(p, dtype, head_dim, tokens_per_page, static_cast<hipStream_t>(stream)), op);
+  return prefill_call(q_prompt, k_prompt, v_prompt, k_cache_paged, v_cache_paged, nullptr, nullptr, page_table,
+                      context_lens, out, dtype, num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                      tokens_per_page, num_pages, page_table_width, static_cast<hipStream_t>(stream));
+}
+
+int pal_paged_attention_prefill_fp8(const void* q_prompt, const void* k_prompt, const void* v_prompt,
+                                    const void* k_cache_paged, const void* v_cache_paged, const float* k_scales,
+                                    const float* v_scales, const uint32_t* page_table, const int32_t* context_lens,
+                                    void* out, int dtype, int64_t num_query_rows, int64_t num_seqs, int num_q_heads,
+                                    int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
+                                    int64_t page_table_width, void* stream) {
+  if (!k_scales || !v_scales)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention_prefill] fp8 pools need both k_scales and v_scales");
+  return prefill_call(q_prompt, k_prompt, v_prompt, k_cache_paged, v_cache_paged, k_scales, v_scales, page_table,
+                      context_lens, out, dtype, num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                      tokens_per_page, num_pages, page_table_width, static_cast<hipStream_t>(stream));
 }
 
 size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, int num_kv_heads,
                                           int head_dim, int tokens_per_page) {
-  if (!valid_dtype(dtype) || num_query_rows <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
-      num_q_heads % num_kv_heads != 0 || !prefill_head_dim_supported(head_dim) ||
-      (tokens_per_page != 16 && tokens_per_page != 32) || num_query_rows > 0x7fffffffLL)
-    return 0;
-  const int group = num_q_heads / num_kv_heads;
-  int resident = 0;
-  int64_t vw = 0;
-  if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
-                     true, false, &resident, &vw) != PAL_OK)
-    return 0;
-  return decode_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
+  return fused_workspace_size(dtype, num_query_rows, num_q_heads, num_kv_heads, head_dim, tokens_per_page, false);
+}
+
+size_t pal_paged_attention_fp8_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, int num_kv_heads,
+                                              int head_dim, int tokens_per_page) {
+  return fused_workspace_size(dtype, num_query_rows, num_q_heads, num_kv_heads, head_dim, tokens_per_page, true);
 }
 
 int pal_paged_attention(const void* queries, const void* k_pool, const void* v_pool, const uint32_t* page_table,
@@ -642,97 +794,24 @@ int pal_paged_attention(const void* queries, const void* k_pool, const void* v_p
                         int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page,
                         int64_t num_pages, int64_t page_table_width, void* workspace, size_t workspace_bytes,
                         void* stream) {
-  const char* op = "paged_attention";
-  int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
-                                page_table_width);
-  if (st != PAL_OK) return st;
-  if (num_query_rows < 0 || num_seqs < 0) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] negative dimension", op);
-  if (!prefill_head_dim_supported(head_dim))
-    return fail(PAL_ERR_RUNTIME, "[%s] no kernel for head_dim %d (supported: 32, 64, 96, 128, 256)", op, head_dim);
-  if (num_query_rows > 0x7fffffffLL || num_seqs > 0x7fffffffLL)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
-  if (num_query_rows == 0) return ok();
-  if (num_pages == 0) page_table_width = 0;  // no page to read: every row is empty
-  if (!queries || !sequence_lengths || !query_to_seq_map || !query_token_offset || !out ||
-      (num_pages > 0 && (!k_pool || !v_pool)) || (page_table_width > 0 && !page_table))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
-  if (!aligned16(queries) || !aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] queries and pools must be 16-byte aligned, out 8-byte aligned", op);
-  const int group = num_q_heads / num_kv_heads;
-  const int hg_max = group < 16 ? group : 16;
-  const int chunks = (group + 15) / 16;
-  int resident = 0;
-  int64_t vw = 0;
-  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, true, false,
-                      &resident,
-                      &vw);
-  if (st != PAL_OK) return st;
-  const DecodeLayout lay = decode_layout(num_query_rows, head_dim, hg_max, vw);
-  if (workspace == nullptr || workspace_bytes < lay.total)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace of %zu bytes needed, %zu given", op, lay.total,
-                workspace_bytes);
-  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] workspace must be 256-byte aligned", op);
-  const hipStream_t hs = static_cast<hipStream_t>(stream);
-  const int qt = pal::prefill_tokens_per_tile(group);
-  const int64_t windows = (num_query_rows + qt - 1) / qt;
-  if (windows * num_kv_heads * chunks > 0x7fffffffLL)
-    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] problem too large for one call", op);
+  return fused_call(queries, k_pool, v_pool, nullptr, nullptr, page_table, sequence_lengths, query_to_seq_map,
+                    query_token_offset, out, dtype, num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                    tokens_per_page, num_pages, page_table_width, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream));
+}
 
-  // 1. runs of rows of one sequence: MFMA tiles over windows of rows
-  pal::PrefillParams pp;
-  pp.q = static_cast<const uint16_t*>(queries);
-  pp.out = static_cast<uint16_t*>(out);
-  pp.k_pool = static_cast<const uint16_t*>(k_pool);
-  pp.v_pool = static_cast<const uint16_t*>(v_pool);
-  pp.k_dense = nullptr;
-  pp.v_dense = nullptr;
-  pp.page_table = page_table;
-  pp.seq_lens = sequence_lengths;
-  pp.q_offset = query_token_offset;
-  pp.q2seq = query_to_seq_map;
-  pp.num_rows = num_query_rows;
-  pp.num_seqs = num_seqs;
-  pp.num_pages = num_pages;
-  pp.page_table_width = page_table_width;
-  pp.num_units = static_cast<int>(windows);
-  pp.prompt_len = 0;
-  pp.num_q_heads = num_q_heads;
-  pp.num_kv_heads = num_kv_heads;
-  pp.group = group;
-  pp.head_chunks = chunks;
-  pp.hg_max = hg_max;
-  pp.scale_log2 = scale_log2_for(head_dim);
-  pp.scale_inv_log2 = 1.f / pp.scale_log2;
-  // 2. rows alone in their run: split-K decode
-  pal::DecodeParams dp = decode_params(queries, k_pool, v_pool, page_table, sequence_lengths, out,
-                                       static_cast<char*>(workspace), lay, num_query_rows, num_pages,
-                                       page_table_width, num_q_heads, num_kv_heads, head_dim, resident, 0);
-  dp.q2seq = query_to_seq_map;
-  dp.q_offset = query_token_offset;
-  dp.num_pt_rows = num_seqs;
-
-  // The decode grid (one persistent workgroup per CU) is launched first on
-  // the caller's stream, then the prefill tiles on the side stream fill the
-  // remaining slots; the caller's stream waits for both.
-  int dev = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return hip_status(err, op);
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  SideStream* ss = nullptr;
-  err = side_stream(dev, &ss);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = hipEventRecord(ss->fork, hs);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = hipStreamWaitEvent(ss->stream, ss->fork, 0);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = pal::launch_decode(dp, dtype, head_dim, tokens_per_page, true, hs);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, ss->stream);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = hipEventRecord(ss->join, ss->stream);
-  if (err != hipSuccess) return hip_status(err, op);
-  return hip_status(hipStreamWaitEvent(hs, ss->join, 0), op);
+int pal_paged_attention_fp8(const void* queries, const void* k_pool, const void* v_pool, const float* k_scales,
+                            const float* v_scales, const uint32_t* page_table, const int32_t* sequence_lengths,
+                            const uint32_t* query_to_seq_map, const int32_t* query_token_offset, void* out, int dtype,
+                            int64_t num_query_rows, int64_t num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                            int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (!k_scales || !v_scales)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[paged_attention] fp8 pools need both k_scales and v_scales");
+  return fused_call(queries, k_pool, v_pool, k_scales, v_scales, page_table, sequence_lengths, query_to_seq_map,
+                    query_token_offset, out, dtype, num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                    tokens_per_page, num_pages, page_table_width, workspace, workspace_bytes,
+                    static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

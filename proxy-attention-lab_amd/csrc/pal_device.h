@@ -103,6 +103,21 @@ struct Dt<kF16> {
   }
 };
 
+// Eight fp8 e4m3 values (w: bytes 0..7) times scale s, as packed 16-bit
+// values of dtype DT (round to nearest even).
+template <int DT>
+__device__ __forceinline__ u32x4 fp8x8_scaled(u32x2 w, float s) {
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t word = q < 2 ? w.x : w.y;
+    const f32x2 f = (q & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(word), true)
+                            : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(word), false);
+    r[q] = Dt<DT>::pack2(f[0] * s, f[1] * s);
+  }
+  return r;
+}
+
 // s_waitcnt immediates (gfx9 encoding): vmcnt <= n only, and lgkmcnt(0) only.
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int kLgkmZero = 15 | (3 << 14) | (7 << 4);

@@ -110,8 +110,10 @@ hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tok
 struct PrefillParams {
   const uint16_t* q;           // [R, Hq, HD]
   uint16_t* out;               // [R, Hq, HD]
-  const uint16_t* k_pool;      // [P, Hkv, HD/8, TPP, 8]
+  const uint16_t* k_pool;      // [P, Hkv, HD/8, TPP, 8] (fp8 pools: [P, Hkv, HD/16, TPP, 16] bytes)
   const uint16_t* v_pool;      // [P, Hkv, HD, TPP]
+  const float* k_scales;       // fp8 pools: [P, Hkv] (null: 16-bit pools of the query dtype)
+  const float* v_scales;
   const uint16_t* k_dense;     // prompt mode: [S * prompt_len, Hkv, HD]
   const uint16_t* v_dense;
   const uint32_t* page_table;  // [S, W]

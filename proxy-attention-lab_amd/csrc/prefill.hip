@@ -124,7 +124,7 @@ struct ItemMap {
 // per tile), query heads h0 .. h0+15 of kv head kvh.  PROMPT: the
 // uniform-prompt mode (keys below the history length from pages, the rest
 // from the dense prompt rows of sequence s); otherwise every key from pages.
-template <int DT, int HD, int TPP, bool PROMPT>
+template <int DT, int HD, int TPP, bool PROMPT, bool KV8>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, int nrows, int64_t s, int kvh, int h0,
                                              uint16_t* k_lds_base, uint16_t* v_lds_base, uint16_t* junk_lds,
                                              uint32_t* pid_lds, int* lim_lds) {
@@ -208,6 +208,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;
   const int64_t page_stride = head_block * p.num_kv_heads;
+  const int64_t page_stride8 = page_stride;            // fp8 pools: bytes per page (one byte per element)
+  const int64_t kv_head_off8 = kvh * head_block;       // and of a kv head's block
   const uint32_t* pt = p.page_table + s * p.page_table_width;
   const int64_t dense_row0 = s * p.prompt_len - hist;  // dense row of key token tok: dense_row0 + tok
   const int64_t dense_stride = static_cast<int64_t>(p.num_kv_heads) * HD;
@@ -243,7 +245,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     const int buf = j % kNBuf;
     const int k0 = j * kKeys;
     if (TPP != 16) pg1 = pg0;
-    const bool fast = k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
+    // fp8 pools take the register path: the copies cannot dequantize
+    const bool fast = !KV8 && k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 &&
+                      (!prompt_mode || k0 + kKeys <= hist);
     if (fast) {
       const int64_t off0 = static_cast<int64_t>(pg0) * page_stride + kv_head_off;
       const int64_t off1 = static_cast<int64_t>(pg1) * page_stride + kv_head_off;
@@ -282,9 +286,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         const int tok = k0 + kj;
         u32x4 val = {0u, 0u, 0u, 0u};
         if (!prompt_mode || tok < hist) {
-          if (pg_ok && tok < max_lim)
-            val = *reinterpret_cast<const u32x4*>(p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off +
-                                                  IM::k_offset(i));
+          if (pg_ok && tok < max_lim) {
+            if constexpr (KV8) {  // dims 8c..8c+7: half of 16-dim stripe c / 2, times the page's K scale
+              const uint8_t* kp8 = reinterpret_cast<const uint8_t*>(p.k_pool) + static_cast<int64_t>(pg) * page_stride8 +
+                                   kv_head_off8 + ((c >> 1) * TPP + kj % TPP) * 16 + (c & 1) * 8;
+              val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(kp8),
+                                     p.k_scales[static_cast<int64_t>(pg) * p.num_kv_heads + kvh]);
+            } else {
+              val = *reinterpret_cast<const u32x4*>(p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off +
+                                                    IM::k_offset(i));
+            }
+          }
         } else if (tok < max_lim) {
           val = *reinterpret_cast<const u32x4*>(p.k_dense + (dense_row0 + tok) * dense_stride + kvh * HD + c * 8);
         }
@@ -296,9 +308,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         IM::v_item(i, d, key);
         const int tok = k0 + key;
         const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off + d * TPP;
+        const uint8_t* vpage8 = reinterpret_cast<const uint8_t*>(p.v_pool) + static_cast<int64_t>(pg) * page_stride8 +
+                                kv_head_off8 + d * TPP;
+        const float vsc = KV8 && pg_ok ? p.v_scales[static_cast<int64_t>(pg) * p.num_kv_heads + kvh] : 1.f;
         u32x4 val = {0u, 0u, 0u, 0u};
         if (!prompt_mode || tok + 8 <= hist) {
-          if (pg_ok && tok < max_lim) val = *reinterpret_cast<const u32x4*>(vpage + key % TPP);
+          if (pg_ok && tok < max_lim) {
+            if constexpr (KV8) {
+              val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(vpage8 + key % TPP), vsc);
+            } else {
+              val = *reinterpret_cast<const u32x4*>(vpage + key % TPP);
+            }
+          }
         } else if (tok < max_lim) {
           // some of the 8 keys are prompt tokens (dense, strided by row)
           uint32_t e16[8];
@@ -306,10 +327,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
           for (int e = 0; e < 8; ++e) {
             const int t2 = tok + e;
             const bool pgd = t2 < hist;
-            const uint16_t* src = pgd ? vpage + (key + e) % TPP
-                                      : p.v_dense + (dense_row0 + t2) * dense_stride + kvh * HD + d;
             uint16_t x = 0;
-            if (t2 < max_lim && (!pgd || pg_ok)) x = *src;
+            if (t2 < max_lim && (!pgd || pg_ok)) {
+              if (!pgd) {
+                x = p.v_dense[(dense_row0 + t2) * dense_stride + kvh * HD + d];
+              } else if constexpr (KV8) {
+                const uint32_t code = vpage8[(key + e) % TPP];
+                x = static_cast<uint16_t>(fp8x8_scaled<DT>(u32x2{code, 0u}, vsc)[0] & 0xFFFFu);
+              } else {
+                x = vpage[(key + e) % TPP];
+              }
+            }
             e16[e] = x;
           }
           val = {e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16)};
@@ -546,7 +574,7 @@ __device__ __forceinline__ bool single_row(const uint32_t* q2seq, int64_t r, int
 //  * window mode (fused op): unit = window of `tokens per tile` rows; every
 //    run of rows of one sequence inside the window that is not a lone decode
 //    row is computed as a tile.
-template <int DT, int HD, int TPP>
+template <int DT, int HD, int TPP, bool KV8>
 __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kNBuf * StepGeo<HD>::kItems * 8];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[kNBuf * StepGeo<HD>::kItems * 8];
@@ -565,7 +593,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillP
     const int s = unit / tps;
     const int j = tps - 1 - (unit - s * tps);
     const int row0 = s * p.prompt_len + j * qt;
-    prefill_tile<DT, HD, TPP, true>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, junk_lds,
+    prefill_tile<DT, HD, TPP, true, KV8>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, junk_lds,
                                     pid_lds, lim_lds);
     return;
   }
@@ -580,37 +608,45 @@ __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillP
     while (end < w1 && !run_start[end - w0]) ++end;
     end = __builtin_amdgcn_readfirstlane(end);
     if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
-      prefill_tile<DT, HD, TPP, false>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
+      prefill_tile<DT, HD, TPP, false, KV8>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
                                        lim_lds);
     cur = end;
   }
 }
 
-template <int DT, int HD, int TPP>
+template <int DT, int HD, int TPP, bool KV8>
 hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
   const int64_t blocks = static_cast<int64_t>(p.num_units) * p.num_kv_heads * p.head_chunks;
-  hipLaunchKernelGGL((prefill_tile_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(blocks)), dim3(kPfThreads), 0,
-                     stream, p);
+  hipLaunchKernelGGL((prefill_tile_kernel<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(blocks)), dim3(kPfThreads),
+                     0, stream, p);
   return hipGetLastError();
 }
 
-template <int DT, int HD>
+template <int DT, int HD, bool KV8>
 hipError_t prefill_tpp(const PrefillParams& p, int tpp, hipStream_t stream) {
   switch (tpp) {
-    case 16: return launch_prefill_t<DT, HD, 16>(p, stream);
-    case 32: return launch_prefill_t<DT, HD, 32>(p, stream);
+    case 16: return launch_prefill_t<DT, HD, 16, KV8>(p, stream);
+    case 32: return launch_prefill_t<DT, HD, 32, KV8>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int DT>
 hipError_t prefill_hd(const PrefillParams& p, int hd, int tpp, hipStream_t stream) {
+  if (p.k_scales) {  // fp8 pools: head dims of whole 16-dim stripes
+    switch (hd) {
+      case 64: return prefill_tpp<DT, 64, true>(p, tpp, stream);
+      case 128: return prefill_tpp<DT, 128, true>(p, tpp, stream);
+      case 256: return prefill_tpp<DT, 256, true>(p, tpp, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (hd) {
-    case 32: return prefill_tpp<DT, 32>(p, tpp, stream);
-    case 64: return prefill_tpp<DT, 64>(p, tpp, stream);
-    case 96: return prefill_tpp<DT, 96>(p, tpp, stream);
-    case 128: return prefill_tpp<DT, 128>(p, tpp, stream);
-    case 256: return prefill_tpp<DT, 256>(p, tpp, stream);
+    case 32: return prefill_tpp<DT, 32, false>(p, tpp, stream);
+    case 64: return prefill_tpp<DT, 64, false>(p, tpp, stream);
+    case 96: return prefill_tpp<DT, 96, false>(p, tpp, stream);
+    case 128: return prefill_tpp<DT, 128, false>(p, tpp, stream);
+    case 256: return prefill_tpp<DT, 256, false>(p, tpp, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -88,6 +88,20 @@ _SIGNATURES = {
         _c_int,
         [_c_void_p] * 8 + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_void_p],
     ),
+    "pal_paged_attention_prefill_fp8": (
+        _c_int,
+        [_c_void_p] * 10 + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_void_p],
+    ),
+    "pal_paged_attention_fp8_workspace_size": (
+        _c_size_t,
+        [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int],
+    ),
+    "pal_paged_attention_fp8": (
+        _c_int,
+        [_c_void_p] * 10
+        + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64]
+        + [_c_void_p, _c_size_t, _c_void_p],
+    ),
     "pal_paged_attention_workspace_size": (
         _c_size_t,
         [_c_int, _c_i64, _c_int, _c_int, _c_int, _c_int],

@@ -486,6 +486,9 @@ def paged_attention_prefill(
     page_table: torch.Tensor,
     context_len_arr: torch.Tensor,
     stream=None,
+    *,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal prefill of a uniform prompt per sequence over a paged history.
 
@@ -499,15 +502,15 @@ def paged_attention_prefill(
     [0, context_len_arr[s]) of its pages and to prompt tokens 0..i.
     Returns [N * Hq, HD], row (s*P + i) * Hq + h; rows past S*P (when N is
     not a multiple of S) are zero.  HD % 32 == 0.  The prompt's K/V need not
-    be in the pages.
+    be in the pages.  fp8 history pools (an addition) need ``k_scales`` /
+    ``v_scales`` (float32 [num_pages, Hkv]); head_dim 64, 128 or 256.
     """
     op = "paged_attention_prefill"
     _require_device("q_prompt", q_prompt)
     device = q_prompt.device
     code = dtype_code(q_prompt.dtype)
     num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_paged, v_cache_paged, device, q_prompt.dtype)
-    if k_cache_paged.dtype == FP8_DTYPE:
-        raise ValueError(f"[{op}] fp8 pools are not supported by this operator")
+    ks, vs = _scales(op, k_cache_paged, k_scales, v_scales, num_pages, num_kv_heads, device)
     num_rows, num_q_heads = _query_dims(op, q_prompt, head_dim)
     for name, t in (("k_prompt", k_prompt), ("v_prompt", v_prompt)):
         _require_device(name, t, device)
@@ -534,10 +537,16 @@ def paged_attention_prefill(
         out = torch.empty((num_rows * num_q_heads, head_dim), dtype=q_prompt.dtype, device=device)
         if covered < num_rows:
             out[covered * num_q_heads:].zero_()
-        status = _lib.lib().pal_paged_attention_prefill(
-            _ptr(q), _ptr(kd), _ptr(vd), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(ctx), _ptr(out),
-            code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width, sh,
-        )
+        if ks is not None:
+            status = _lib.lib().pal_paged_attention_prefill_fp8(
+                _ptr(q), _ptr(kd), _ptr(vd), _ptr(kp), _ptr(vp), _ptr(ks.contiguous()), _ptr(vs.contiguous()),
+                _ptr(pt), _ptr(ctx), _ptr(out), code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
+                num_pages, width, sh)
+        else:
+            status = _lib.lib().pal_paged_attention_prefill(
+                _ptr(q), _ptr(kd), _ptr(vd), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(ctx), _ptr(out),
+                code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width, sh,
+            )
     _lib.check(status)
     return out
 
@@ -551,6 +560,9 @@ def paged_attention(
     query_to_seq_map: torch.Tensor,
     query_token_offset: torch.Tensor,
     stream=None,
+    *,
+    k_scales: torch.Tensor | None = None,
+    v_scales: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Fused mixed batch: decode rows and prefill rows in one call.
 
@@ -563,15 +575,15 @@ def paged_attention(
     token at absolute position p passes p + 1 (its K/V already written by
     fill_kv_pages).  Returns [R, Hq, HD]; rows that see no token, or name no
     sequence, are zero.  Runs of consecutive rows of one sequence run as MFMA
-    prefill tiles, single rows on the split-K decode path.
+    prefill tiles, single rows on the split-K decode path.  fp8 pools need
+    ``k_scales`` / ``v_scales`` (float32 [num_pages, Hkv]).
     """
     op = "paged_attention"
     _require_device("queries", queries)
     device = queries.device
     code = dtype_code(queries.dtype)
     num_pages, num_kv_heads, head_dim, tpp = _pools(op, k_cache_pool, v_cache_pool, device, queries.dtype)
-    if k_cache_pool.dtype == FP8_DTYPE:
-        raise ValueError(f"[{op}] fp8 pools are not supported by this operator")
+    ks, vs = _scales(op, k_cache_pool, k_scales, v_scales, num_pages, num_kv_heads, device)
     num_rows, num_q_heads = _query_dims(op, queries, head_dim)
     if page_table.dim() != 2:
         raise ValueError(f"[{op}] page_table must be 2D [num_seqs, max_pages_per_seq]")
@@ -596,14 +608,21 @@ def paged_attention(
         out = torch.empty((num_rows, num_q_heads, head_dim), dtype=queries.dtype, device=device)
         ws = None
         if num_rows > 0:
+            size_fn = L.pal_paged_attention_fp8_workspace_size if ks is not None else \
+                L.pal_paged_attention_workspace_size
             with torch.cuda.device(device):
-                ws_bytes = L.pal_paged_attention_workspace_size(code, num_rows, num_q_heads, num_kv_heads, head_dim,
-                                                                tpp)
+                ws_bytes = size_fn(code, num_rows, num_q_heads, num_kv_heads, head_dim, tpp)
             ws = _workspace("fused", ws_bytes, device, sh)
-        status = L.pal_paged_attention(
-            _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(q2s), _ptr(off), _ptr(out),
-            code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width,
-            _ptr(ws), ws.numel() if ws is not None else 0, sh,
-        )
+        if ks is not None:
+            status = L.pal_paged_attention_fp8(
+                _ptr(q), _ptr(kp), _ptr(vp), _ptr(ks.contiguous()), _ptr(vs.contiguous()), _ptr(pt), _ptr(lens),
+                _ptr(q2s), _ptr(off), _ptr(out), code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp,
+                num_pages, width, _ptr(ws), ws.numel() if ws is not None else 0, sh)
+        else:
+            status = L.pal_paged_attention(
+                _ptr(q), _ptr(kp), _ptr(vp), _ptr(pt), _ptr(lens), _ptr(q2s), _ptr(off), _ptr(out),
+                code, num_rows, num_seqs, num_q_heads, num_kv_heads, head_dim, tpp, num_pages, width,
+                _ptr(ws), ws.numel() if ws is not None else 0, sh,
+            )
     _lib.check(status)
     return out

@@ -2,9 +2,10 @@
 
 Pools after fill_kv_pages (fp8, or 16-bit from fp32 / other-dtype rows) and
 after rope_fill_kv_pages, and the rotated queries, must be bit-exact against
-the oracle (oracle.fill_kv_pages_ex).  Decode over fp8 pools is compared with
-the oracle on the dequantized pools (code x scale of its (page, kv head)) at
-the query dtype's attention tolerance: bf16 atol/rtol 2e-2, fp16 5e-3.
+the oracle (oracle.fill_kv_pages_ex).  Decode, prefill and the fused mixed
+batch over fp8 pools are compared with the oracle on the dequantized pools
+(code x scale of its (page, kv head)) at the query dtype's attention
+tolerance: bf16 atol/rtol 2e-2, fp16 5e-3.
 """
 
 from __future__ import annotations
@@ -267,3 +268,50 @@ def test_fill_fp8_then_decode_round_trip():
     assert np.array_equal(host_codes(kd), ek) and np.array_equal(host_codes(vd), ev)
     ref = orc.paged_attention_decode(q, ek, ev, case.page_table, lens, "bf16", kv_scales=(ks, vs))
     assert_close(host_f32(out), ref, "bf16", "fp8 fill + decode")
+
+
+# ---------------------------------------------------------------------------
+# prefill and the fused mixed batch over fp8 pools
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("hd,tpp", [(128, 16), (64, 32), (256, 16)])
+def test_prefill_fp8_history(dtype, hd, tpp):
+    """The reference prefill signature over an fp8 history (dense prompt in
+    the query dtype): history keys straddling the prompt, ragged histories."""
+    from pal_cases import make_prefill_case
+
+    rng = np.random.default_rng(hd + tpp + 7)
+    case, q, k, v = make_prefill_case(hd * 5 + tpp, [0, 37, 300, 1000], 45, 16, 4, hd, tpp, dtype)
+    kc, vc, ks, vs = fp8_case(case, rng)
+    announce(f"prefill fp8 history {dtype} hd={hd} tpp={tpp}")
+    out = pal.paged_attention_prefill(dev_bits(q, dtype), dev_bits(k, dtype), dev_bits(v, dtype), dev_codes(kc),
+                                      dev_codes(vc), dev_index(case.page_table, torch.uint32), dev_index(case.seq_lens),
+                                      k_scales=torch.from_numpy(ks).to(DEV), v_scales=torch.from_numpy(vs).to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.paged_attention_prefill(q, k, v, kc, vc, case.page_table, case.seq_lens, dtype, kv_scales=(ks, vs))
+    assert_close(host_f32(out), ref, dtype, f"fp8 prefill {dtype} hd{hd} tpp{tpp}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("hd,tpp", [(128, 16), (64, 32), (256, 16)])
+def test_fused_fp8_pages(dtype, hd, tpp):
+    """A mixed batch over fp8 pages: decode rows (the fused op's shared-CU
+    decode, or the stream kernel at head_dim 256) and prefill runs."""
+    from pal_cases import make_fused_case
+
+    rng = np.random.default_rng(hd * 3 + tpp)
+    fc = make_fused_case(hd + tpp + 11, [1, 17, 300, 2049, 0, 700], [(0, 70), (130, 64), (900, 129)], 32, 8, hd,
+                         tpp, dtype, block=40)
+    c = fc.case
+    kc, vc, ks, vs = fp8_case(c, rng)
+    announce(f"fused fp8 pages {dtype} hd={hd} tpp={tpp}")
+    out = pal.paged_attention(dev_bits(fc.queries, dtype), dev_codes(kc), dev_codes(vc),
+                              dev_index(c.page_table, torch.uint32), dev_index(c.seq_lens),
+                              dev_index(fc.q2seq, torch.uint32), dev_index(fc.q_offset),
+                              k_scales=torch.from_numpy(ks).to(DEV), v_scales=torch.from_numpy(vs).to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.paged_attention(fc.queries, kc, vc, c.page_table, c.seq_lens, fc.q2seq, fc.q_offset, dtype,
+                              kv_scales=(ks, vs))
+    assert_close(host_f32(out), ref, dtype, f"fp8 fused {dtype} hd{hd} tpp{tpp}")
