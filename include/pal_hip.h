@@ -301,6 +301,70 @@ int pal_paged_attention_fp8(const void* queries, const void* k_pool, const void*
                             int tokens_per_page, int64_t num_pages, int64_t page_table_width, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/*
+ * Page-pool allocator and compaction.  No reference counterpart: the
+ * reference takes page tables from its caller (ops.py:61-63,
+ * paged_attention_decode_primitive.cpp:71-266 reads them as an input); this
+ * is the allocator a serving engine keeps in front of the pools.  Host-side
+ * state, internally locked.
+ *
+ * pal_page_pool_create: a pool of num_pages free page ids (< 2^32).
+ * pal_page_pool_alloc: the n lowest free ids, ascending, into out_ids; fails
+ *   with PAL_ERR_RUNTIME (and allocates nothing) when fewer are free.
+ * pal_page_pool_free: returns ids; an id out of range, not allocated or
+ *   listed twice fails the whole call (PAL_ERR_INVALID_ARGUMENT), nothing
+ *   freed.
+ * pal_page_pool_num_free: free ids (negative status for a null pool).
+ * pal_page_pool_compaction_plan: moves every allocated id at or above L
+ *   (the number of allocated ids) to a free id below L, both in ascending
+ *   order, so the allocated ids become exactly [0, L); writes the moves to
+ *   src / dst (host arrays of `capacity` entries) and their count to
+ *   *n_moves, and updates the allocator.  With src = dst = NULL and
+ *   capacity 0 it only reports the count.  Apply the moves with
+ *   pal_copy_pages, then rewrite page tables with pal_remap_pages.
+ */
+int pal_page_pool_create(int64_t num_pages, void** pool);
+int pal_page_pool_destroy(void* pool);
+int pal_page_pool_alloc(void* pool, int64_t n, uint32_t* out_ids);
+int pal_page_pool_free(void* pool, const uint32_t* ids, int64_t n);
+int64_t pal_page_pool_num_free(void* pool);
+int pal_page_pool_compaction_plan(void* pool, uint32_t* src, uint32_t* dst, int64_t capacity, int64_t* n_moves);
+
+/*
+ * Copies pages src[m] -> dst[m] (device arrays, num_moves entries) of both
+ * pools, page_bytes bytes per page and pool (Hkv * HD * TPP * element size),
+ * and for fp8 pools the scale rows (k_scales / v_scales [num_pages, Hkv],
+ * both or neither).  Ids >= num_pages are skipped.  Sources and
+ * destinations must be disjoint sets (a compaction plan is).  Bit-exact.
+ */
+int pal_copy_pages(void* k_pool, void* v_pool, float* k_scales, float* v_scales, int64_t num_pages, int num_kv_heads,
+                   int64_t page_bytes, const uint32_t* src, const uint32_t* dst, int64_t num_moves, void* stream);
+
+/*
+ * In place over num_entries page ids (device): id -> remap[id] for
+ * id < remap_len, other ids unchanged.
+ */
+int pal_remap_pages(uint32_t* page_table, int64_t num_entries, const uint32_t* remap, int64_t remap_len,
+                    void* stream);
+
+/*
+ * Debug checks.  A library built with PAL_DEBUG_CHECKS (build_lib.py
+ * --debug-checks: libpal_hip_debug.so) records, instead of silently
+ * tolerating, inputs the caller most likely did not mean: a page id past
+ * the pool where a token was to be read (PAL_DEBUG_PAGE_ID), a sequence
+ * length or history past page_table_width * tokens_per_page
+ * (PAL_DEBUG_LENGTH), a fill token with no valid destination
+ * (PAL_DEBUG_FILL_DEST).  pal_debug_flags waits for nothing: call it after
+ * synchronising; it ORs the recorded bits into *flags and, with reset,
+ * clears them.  No reference counterpart (the reference's Debug build only
+ * adds host-side checks, src/pal_core/CMakeLists.txt:16-31).  A release
+ * build returns PAL_ERR_RUNTIME and flags 0.
+ */
+#define PAL_DEBUG_PAGE_ID 1u
+#define PAL_DEBUG_LENGTH 2u
+#define PAL_DEBUG_FILL_DEST 4u
+int pal_debug_flags(int reset, uint32_t* flags);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,10 @@ It restates, in numpy, what the reference computes on the hot path:
   pages (no reference counterpart: the reference stores f16 / bf16 only,
   paged_attention_kernels.metal:41-42); OCP e4m3 "fn" (bias 7, 3 mantissa
   bits, max 448, no infinities), round to nearest even.
+* ``compaction_plan`` / ``apply_moves`` / ``remap_table`` -- the page-pool
+  compaction (no reference counterpart); pinned by its invariants: the live
+  set becomes [0, L), ids below L stay put, every page's bytes follow it,
+  and attention through the remapped tables is unchanged.
 * ``rope_cos_sin_cache`` / ``apply_rope`` / ``fill_kv_pages_ex`` -- the step
   feeding fill_kv_pages (RoPE of K and Q, cast to the pool dtype) fused with
   its scatter; the scatter is that of fill_kv_pages.h.metal:65-116 with the
@@ -521,6 +525,42 @@ def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offs
         k, v = gather_tokens(kf, vf, pt[s], n)
         out[rows] = attend(q[rows], k, v, limits)
     return out
+
+
+# ---------------------------------------------------------------------------
+# page-pool compaction (no reference counterpart: the reference's page
+# tables come from the caller, ops.py:61-63)
+# ---------------------------------------------------------------------------
+
+
+def compaction_plan(used: np.ndarray, num_pages: int):
+    """Moves that make the allocated ids exactly [0, L), L = len(used): every
+    allocated id >= L, ascending, goes to the free ids < L, ascending.
+    Returns (src, dst) uint32 arrays."""
+    used = np.unique(np.asarray(used, np.int64))
+    live = len(used)
+    is_used = np.zeros(num_pages, bool)
+    is_used[used] = True
+    movers = np.nonzero(is_used[live:])[0] + live
+    holes = np.nonzero(~is_used[:live])[0]
+    assert len(movers) == len(holes)
+    return movers.astype(np.uint32), holes.astype(np.uint32)
+
+
+def apply_moves(pool: np.ndarray, src, dst) -> np.ndarray:
+    """A copy of a pool (pages along axis 0) with page src[m] copied to
+    dst[m]; sources and destinations disjoint."""
+    out = np.array(pool, copy=True)
+    out[np.asarray(dst, np.int64)] = np.asarray(pool)[np.asarray(src, np.int64)]
+    return out
+
+
+def remap_table(table, src, dst, num_pages: int) -> np.ndarray:
+    """Page table with id src[m] replaced by dst[m] (ids >= num_pages kept)."""
+    remap = np.arange(num_pages, dtype=np.int64)
+    remap[np.asarray(src, np.int64)] = np.asarray(dst, np.int64)
+    t = np.asarray(table).astype(np.int64)
+    return np.where(t < num_pages, remap[np.minimum(t, num_pages - 1)], t).astype(np.asarray(table).dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -52,6 +52,9 @@
 
 namespace pal {
 
+// flag word of this translation unit's debug checks (see pal_device.h)
+PAL_DEBUG_FLAGS_DEFINE(decode_debug_flags)
+
 namespace {
 
 constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
@@ -95,6 +98,7 @@ __device__ __forceinline__ Item item_at(const DecodeParams& p, int64_t i, int tp
     len = p.seq_lens[i];
   }
   const int64_t max_tokens = p.page_table_width * tpp;
+  PAL_DEBUG_FLAG(len > max_tokens, kDebugLength);
   it.len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
   return it;
 }
@@ -416,6 +420,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       const uint32_t win = to_next ? w_n0 : ((e >> 6) == wcur ? w_c : w_x);
       const uint32_t pg = __builtin_amdgcn_readlane(win, static_cast<int>(e & 63));
       bv[buf] = pg < p.num_pages;
+      PAL_DEBUG_FLAG(!bv[buf] && (to_next ? i - n_pad < nblk_n : i < n_blk), kDebugPageId);
       const uint32_t page = bv[buf] ? pg : 0u;
       const int slot0 = static_cast<int>((b * 16) % TPP);
       const uint8_t* kb_x = kbase_n;

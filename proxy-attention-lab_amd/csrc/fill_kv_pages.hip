@@ -41,6 +41,9 @@
 
 namespace pal {
 
+// flag word of this translation unit's debug checks (see pal_device.h)
+PAL_DEBUG_FLAGS_DEFINE(fill_debug_flags)
+
 namespace {
 
 #ifndef PAL_FILL_THREADS
@@ -359,6 +362,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
         }
       }
     }
+    PAL_DEBUG_FLAG(tid < nwin && dslot < 0, kDebugFillDest);
     page_lds[tid] = dpage;
     slot_lds[tid] = dslot;
     pos_lds[tid] = pos;

@@ -16,10 +16,9 @@
 
 #include "../../include/pal_hip.h"
 #include "pal_hip_internal.h"
+#include "pal_log.h"
 
 namespace {
-
-thread_local std::string g_last_error;
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -27,12 +26,12 @@ int fail(int code, const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
-  g_last_error = buf;
+  pal::set_last_error(buf);
   return code;
 }
 
 int ok() {
-  g_last_error.clear();
+  pal::clear_last_error();
   return PAL_OK;
 }
 
@@ -304,6 +303,10 @@ int fill_call(const char* op, const FillArgs& a, hipStream_t stream) {
   p.q_out_dtype = a.q_out_dtype;
   p.rope_style = a.rope_style;
   p.rotary_dim = a.rope_style != 0 ? a.rotary_dim : 0;
+  PAL_LOG("%s tokens=%lld Hkv=%d HD=%d TPP=%d src=%d kv=%d rope=%d/%d queries=%d pages=%lld stream=%p", op,
+          static_cast<long long>(a.num_tokens), a.num_kv_heads, a.head_dim, a.tokens_per_page, a.src_dtype,
+          a.kv_dtype, a.rope_style, p.rotary_dim, a.queries ? a.num_q_heads : 0, static_cast<long long>(a.num_pages),
+          static_cast<void*>(stream));
   return hip_status(pal::launch_fill_kv_pages(p, stream), op);
 }
 
@@ -374,6 +377,9 @@ int prefill_call(const void* q_prompt, const void* k_prompt, const void* v_promp
   p.hg_max = hg_max;
   p.scale_log2 = scale_log2_for(head_dim);
   p.scale_inv_log2 = 1.f / p.scale_log2;
+  PAL_LOG("%s rows=%lld seqs=%lld P=%d Hq=%d Hkv=%d HD=%d TPP=%d dtype=%d fp8=%d tiles=%d stream=%p", op,
+          static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs), p.prompt_len, num_q_heads,
+          num_kv_heads, head_dim, tokens_per_page, dtype, k_scales ? 1 : 0, p.num_units, static_cast<void*>(stream));
   return hip_status(pal::launch_prefill(p, dtype, head_dim, tokens_per_page, stream), op);
 }
 
@@ -475,6 +481,10 @@ int fused_call(const void* queries, const void* k_pool, const void* v_pool, cons
   dp.q_offset = query_token_offset;
   dp.num_pt_rows = num_seqs;
 
+  PAL_LOG("%s rows=%lld seqs=%lld Hq=%d Hkv=%d HD=%d TPP=%d dtype=%d fp8=%d windows=%lld decode_workers=%d stream=%p",
+          op, static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs), num_q_heads, num_kv_heads,
+          head_dim, tokens_per_page, dtype, kv8 ? 1 : 0, static_cast<long long>(windows), resident,
+          static_cast<void*>(hs));
   // The decode grid (one persistent workgroup per CU) is launched first on
   // the caller's stream, then the prefill tiles on the side stream fill the
   // remaining slots; the caller's stream waits for both.
@@ -571,6 +581,11 @@ int decode_call(const void* queries, const void* k_pool, const void* v_pool, con
                                       num_q_heads, num_kv_heads, head_dim, resident, partition_size);
   p.k_scales = k_scales;
   p.v_scales = v_scales;
+  PAL_LOG("paged_attention_decode seqs=%lld Hq=%d Hkv=%d HD=%d TPP=%d W=%lld dtype=%d fp8=%d partition=%d "
+          "workers=%d virtual=%lld ws=%zu scratch=%d stream=%p",
+          static_cast<long long>(num_seqs), num_q_heads, num_kv_heads, head_dim, tokens_per_page,
+          static_cast<long long>(page_table_width), dtype, kv8 ? 1 : 0, partition_size, resident,
+          static_cast<long long>(vw), lay.total, use_scratch ? 1 : 0, static_cast<void*>(stream));
   return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, false, stream),
                     "paged_attention_decode");
 }
@@ -579,7 +594,7 @@ int decode_call(const void* queries, const void* k_pool, const void* v_pool, con
 
 extern "C" {
 
-const char* pal_last_error(void) { return g_last_error.c_str(); }
+const char* pal_last_error(void) { return pal::last_error(); }
 
 const char* pal_version(void) { return "2025.06.4+gfx950"; }
 
@@ -812,6 +827,58 @@ int pal_paged_attention_fp8(const void* queries, const void* k_pool, const void*
                     query_token_offset, out, dtype, num_query_rows, num_seqs, num_q_heads, num_kv_heads, head_dim,
                     tokens_per_page, num_pages, page_table_width, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream));
+}
+
+int pal_copy_pages(void* k_pool, void* v_pool, float* k_scales, float* v_scales, int64_t num_pages, int num_kv_heads,
+                   int64_t page_bytes, const uint32_t* src, const uint32_t* dst, int64_t num_moves, void* stream) {
+  const char* op = "copy_pages";
+  if (num_moves < 0 || num_pages < 0 || num_kv_heads <= 0 || num_kv_heads > 256 || page_bytes <= 0 ||
+      page_bytes % 16 != 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] bad dimensions (page_bytes must be a positive multiple of 16)", op);
+  if (num_moves == 0) return ok();
+  if (!k_pool || !v_pool || !src || !dst || (!k_scales != !v_scales))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] null pointer argument", op);
+  if (!aligned16(k_pool) || !aligned16(v_pool))
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] pools must be 16-byte aligned", op);
+  pal::PageCopyParams p;
+  p.k_pool = k_pool;
+  p.v_pool = v_pool;
+  p.k_scales = k_scales;
+  p.v_scales = v_scales;
+  p.src = src;
+  p.dst = dst;
+  p.num_moves = num_moves;
+  p.num_pages = num_pages;
+  p.page_bytes = page_bytes;
+  p.num_kv_heads = num_kv_heads;
+  return hip_status(pal::launch_copy_pages(p, static_cast<hipStream_t>(stream)), op);
+}
+
+int pal_remap_pages(uint32_t* page_table, int64_t num_entries, const uint32_t* remap, int64_t remap_len,
+                    void* stream) {
+  if (num_entries < 0 || remap_len < 0)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[remap_pages] negative size");
+  if (num_entries == 0) return ok();
+  if (!page_table || !remap) return fail(PAL_ERR_INVALID_ARGUMENT, "[remap_pages] null pointer argument");
+  return hip_status(pal::launch_remap_pages(page_table, num_entries, remap, remap_len, static_cast<hipStream_t>(stream)),
+                    "remap_pages");
+}
+
+int pal_debug_flags(int reset, uint32_t* flags) {
+  if (!flags) return fail(PAL_ERR_INVALID_ARGUMENT, "[debug_flags] null output");
+#ifdef PAL_DEBUG_CHECKS
+  uint32_t a = 0, b = 0, c = 0;
+  hipError_t err = pal::decode_debug_flags(&a, reset != 0);
+  if (err == hipSuccess) err = pal::prefill_debug_flags(&b, reset != 0);
+  if (err == hipSuccess) err = pal::fill_debug_flags(&c, reset != 0);
+  if (err != hipSuccess) return hip_status(err, "debug_flags");
+  *flags = a | b | c;
+  return ok();
+#else
+  (void)reset;
+  *flags = 0;
+  return fail(PAL_ERR_RUNTIME, "[debug_flags] this library was built without PAL_DEBUG_CHECKS");
+#endif
 }
 
 }  // extern "C"

@@ -29,6 +29,44 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------------------
+// Debug checks (builds with -DPAL_DEBUG_CHECKS only): a kernel that meets an
+// input it tolerates but that the caller most likely did not mean (a page id
+// past the pool, a length past the page table, a fill destination out of
+// range) sets a bit in its translation unit's flag word instead of silently
+// reading zeros or skipping; pal_debug_flags() reads and clears the words.
+// Nothing traps.  Release builds compile the checks away.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kDebugPageId = 1u;     // a page id >= num_pages where a token was to be read
+constexpr uint32_t kDebugLength = 2u;     // a length or position past page_table_width * TPP
+constexpr uint32_t kDebugFillDest = 4u;   // a fill token with no valid destination (skipped)
+
+#ifdef PAL_DEBUG_CHECKS
+#define PAL_DEBUG_FLAGS_DEFINE(fn)                                                       \
+  namespace {                                                                            \
+  __device__ uint32_t g_debug_flags;                                                     \
+  }                                                                                      \
+  hipError_t fn(uint32_t* out, bool reset) {                                             \
+    hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_debug_flags), sizeof(uint32_t)); \
+    if (e != hipSuccess || !reset) return e;                                             \
+    const uint32_t zero = 0;                                                             \
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_debug_flags), &zero, sizeof(uint32_t));        \
+  }
+#define PAL_DEBUG_FLAG(cond, bit)                      \
+  do {                                                 \
+    if (cond) atomicOr(&g_debug_flags, (bit));         \
+  } while (0)
+#else
+#define PAL_DEBUG_FLAGS_DEFINE(fn)             \
+  hipError_t fn(uint32_t* out, bool) {         \
+    *out = 0;                                  \
+    return hipSuccess;                         \
+  }
+#define PAL_DEBUG_FLAG(cond, bit) \
+  do {                            \
+  } while (0)
+#endif
+
+// ---------------------------------------------------------------------------
 // dtype traits: scalar conversion, packing and the MFMA shapes used here.
 //   mma16x16x32: A[16 x 32] * B[32 x 16] (8 elements per lane per operand)
 //   mma16x16x16: A[16 x 16] * B[16 x 16] (4 elements per lane per operand)

@@ -139,6 +139,32 @@ struct PrefillParams {
 int prefill_tokens_per_tile(int group);
 hipError_t launch_prefill(const PrefillParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
 
+// Page moves of a compaction: pages src[m] -> dst[m] of both pools (whole
+// pages, page_bytes each) and, for fp8 pools, their scale rows.  Sources and
+// destinations must be disjoint sets.
+struct PageCopyParams {
+  void* k_pool;
+  void* v_pool;
+  float* k_scales;  // null: 16-bit pools
+  float* v_scales;
+  const uint32_t* src;  // [num_moves] device
+  const uint32_t* dst;
+  int64_t num_moves;
+  int64_t num_pages;
+  int64_t page_bytes;
+  int num_kv_heads;
+};
+
+hipError_t launch_copy_pages(const PageCopyParams& p, hipStream_t stream);
+hipError_t launch_remap_pages(uint32_t* table, int64_t n, const uint32_t* remap, int64_t remap_len,
+                              hipStream_t stream);
+
+// Debug-check flag words of the kernel translation units (all zero in a
+// build without PAL_DEBUG_CHECKS); reset clears them after reading.
+hipError_t decode_debug_flags(uint32_t* out, bool reset);
+hipError_t prefill_debug_flags(uint32_t* out, bool reset);
+hipError_t fill_debug_flags(uint32_t* out, bool reset);
+
 // Scratch memory held by the library for pal_paged_attention_decode_noalloc:
 // kScratchBytes per device, in a file-scope device array (scratch.hip).
 // scratch_buffer returns its device address on the current device.

@@ -43,6 +43,9 @@
 
 namespace pal {
 
+// flag word of this translation unit's debug checks (see pal_device.h)
+PAL_DEBUG_FLAGS_DEFINE(prefill_debug_flags)
+
 namespace {
 
 constexpr int kPfWaves = 4;
@@ -157,10 +160,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   int64_t slen;
   if (prompt_mode) {
     hist = p.seq_lens[s];
+    PAL_DEBUG_FLAG(hist > max_tokens, kDebugLength);
     hist = hist < 0 ? 0 : (hist > max_tokens ? max_tokens : hist);
     slen = hist + p.prompt_len;
   } else {
     slen = seq_ok ? p.seq_lens[s] : 0;
+    PAL_DEBUG_FLAG(slen > max_tokens, kDebugLength);
     slen = slen < 0 ? 0 : (slen > max_tokens ? max_tokens : slen);
   }
 
@@ -279,6 +284,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       if (i >= NI) continue;
       const uint32_t pg = IM::k_page_half(i) ? pg1 : pg0;
       const bool pg_ok = pg < p.num_pages;
+      PAL_DEBUG_FLAG(!pg_ok && k0 + (IM::k_page_half(i) ? 16 : 0) < (prompt_mode ? min(max_lim, static_cast<int>(hist)) : max_lim),
+                     kDebugPageId);
       // K: stripe c, key kj of the step
       {
         int kj, c;

@@ -12,6 +12,7 @@ from proxy_attention_lab.layout import (
     get_v_cache_shape,
 )
 from proxy_attention_lab.layout import FP8_DTYPE
+from proxy_attention_lab.page_pool import PagePool
 from proxy_attention_lab.ops import (
     fill_kv_pages,
     paged_attention,
@@ -35,4 +36,5 @@ __all__ = [
     "rope_cos_sin_cache",
     "rope_fill_kv_pages",
     "FP8_DTYPE",
+    "PagePool",
 ]

@@ -112,6 +112,18 @@ _SIGNATURES = {
         + [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64]
         + [_c_void_p, _c_size_t, _c_void_p],
     ),
+    "pal_page_pool_create": (_c_int, [_c_i64, ctypes.POINTER(_c_void_p)]),
+    "pal_page_pool_destroy": (_c_int, [_c_void_p]),
+    "pal_page_pool_alloc": (_c_int, [_c_void_p, _c_i64, _c_void_p]),
+    "pal_page_pool_free": (_c_int, [_c_void_p, _c_void_p, _c_i64]),
+    "pal_page_pool_num_free": (_c_i64, [_c_void_p]),
+    "pal_page_pool_compaction_plan": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, ctypes.POINTER(_c_i64)]),
+    "pal_copy_pages": (
+        _c_int,
+        [_c_void_p] * 4 + [_c_i64, _c_int, _c_i64, _c_void_p, _c_void_p, _c_i64, _c_void_p],
+    ),
+    "pal_remap_pages": (_c_int, [_c_void_p, _c_i64, _c_void_p, _c_i64, _c_void_p]),
+    "pal_debug_flags": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_uint32)]),
 }
 
 _lock = threading.Lock()
