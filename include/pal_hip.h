@@ -10,8 +10,7 @@
  * Conventions
  *  - All tensor arguments are raw device pointers to contiguous row-major
  *    buffers allocated by the caller; the library never allocates or frees
- *    device memory (pal_paged_attention creates one side stream and two
- *    events per device on first use).
+ *    device memory.
  *  - fp16 / bf16 data is passed as `void*`, with a dtype code.
  *  - `stream` is a hipStream_t passed as `void*` (NULL = the null stream).
  *    Launches are asynchronous; the caller synchronises.
@@ -273,8 +272,11 @@ size_t pal_paged_attention_workspace_size(int dtype, int64_t num_query_rows, int
  * p + 1.  Rows with no visible token, or naming no sequence (s >= num_seqs),
  * yield zeros.  out: [num_query_rows, num_q_heads, head_dim].  Runs of
  * consecutive rows of one sequence go to MFMA prefill tiles, single rows to
- * the split-K decode kernels; a device-side planner builds that work list,
- * so the call never reads row metadata on the host.  The workspace (size
+ * split-K decode workers, in one kernel whose first workgroups are the decode
+ * workers (head dims up to 128; above, the decode and prefill kernels run one
+ * after the other), followed by the merge kernel; the decode workers find
+ * and schedule the single rows on the device, so the call never reads row
+ * metadata on the host.  The workspace (size
  * from pal_paged_attention_workspace_size, 256-byte aligned, zero-filled
  * before its first use) must not be shared by concurrent calls.
  */

@@ -55,6 +55,12 @@ namespace pal {
 // flag word of this translation unit's debug checks (see pal_device.h)
 PAL_DEBUG_FLAGS_DEFINE(decode_debug_flags)
 
+}  // namespace pal
+
+#include "prefill_tile.h"  // the fused kernel's prefill tiles
+
+namespace pal {
+
 namespace {
 
 constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
@@ -179,7 +185,7 @@ __device__ __forceinline__ int64_t locate_seq(const int64_t* cum, int64_t num_se
 // sequence s (all of its segments), cum[S] = hdr[0] = T.  Each thread takes
 // kPlanPer consecutive items per pass, so their length loads go out together;
 // it also writes the zeros of an empty item.
-constexpr int kPlanPer = 8;
+constexpr int kPlanPer = 16;
 
 template <int HD, int TPP>
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeParams p) {
@@ -227,6 +233,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
 struct ItemLds {
   const int64_t* len;  // null: read items from global memory (item_at)
   const int32_t* seq;
+  const int32_t* row;  // query / output row of each item (null: item s is row s)
 };
 
 // Streams the blocks of virtual workers v_begin .. v_end-1 (one wavefront;
@@ -327,7 +334,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     const int qh_base = (seg / p.head_chunks) * p.group + h0;
     const bool hv = r16 < hg;
     const uint32_t qmask = hv ? 0xFFFFFFFFu : 0u;
-    const uint16_t* qrow = p.q + (s * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
+    const int64_t qr = il.row ? static_cast<int64_t>(il.row[s]) : s;
+    const uint16_t* qrow = p.q + (qr * p.num_q_heads + qh_base + (hv ? r16 : 0)) * HD;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       if constexpr (KV8) {  // k-step kk = (stripe j = kk / 2, half): dims 16 (g + 4j) + 8 half .. +7
@@ -625,7 +633,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
     if (r16 < hg) {
-      const int64_t row = c_s * p.num_q_heads + qh_base + r16;
+      const int64_t row = (il.row ? static_cast<int64_t>(il.row[c_s]) : c_s) * p.num_q_heads + qh_base + r16;
       if (complete) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
@@ -657,7 +665,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     if (!complete && c_blk == 0) {
       list_g0 = c_gpos;  // the piece starts the segment
       list_nb = c_nb;
-      list_row = c_s;
+      list_row = il.row ? static_cast<int64_t>(il.row[c_s]) : c_s;
       list_seg = c_seg;
     }
     prologue = false;
@@ -740,7 +748,7 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
     total = p.hdr[0];
   }
   if (total == 0) return;
-  const ItemLds il = lds_plan ? ItemLds{len_lds, seq_lds} : ItemLds{nullptr, nullptr};
+  const ItemLds il = lds_plan ? ItemLds{len_lds, seq_lds, nullptr} : ItemLds{nullptr, nullptr, nullptr};
   const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
   const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
   if constexpr (kChunks) {
@@ -785,12 +793,11 @@ __global__ __launch_bounds__(kGroupThreads) void decode_stream_kernel(const Deco
 }
 
 // Decode rows of the fused op: one workgroup per CU, held to half of the
-// register file (head_dim 128 with 32-token pages: one block of prefetch)
-// so that a prefill tile wavefront fits on every SIMD beside it and the
-// HBM-bound decode overlaps the MFMA-bound prefill instead of taking turns
-// with it.
-// Head dims above 128 use decode_stream_kernel: their prefill tiles need
-// more than half of the register file themselves.
+// register file (head_dim 128: one block of prefetch), so that a prefill tile
+// wavefront fits on every SIMD beside it and the HBM-bound decode overlaps
+// the MFMA-bound prefill instead of taking turns with it.
+// Head dims above 128 run the two halves one after the other: their prefill
+// tiles need more than half of the register file themselves.
 constexpr bool shares_cu(int hd) { return hd <= 128; }
 
 template <int HD, int TPP>
@@ -798,14 +805,192 @@ constexpr int shared_cu_prefetch() {
   return HD == 128 ? kPrefetch - 1 : kPrefetch;
 }
 
+// The decode rows of the fused op, found and scheduled inside the fused
+// kernel (no planning launch): every decode workgroup scans the query rows,
+// keeps the rows alone in their run of same-sequence rows that have keys
+// ("lone rows"; the prefill tiles take every other row), and compacts up to
+// kFusedLone of them -- row, page-table row, length and first global block --
+// into LDS.  The scan is a pure function of the inputs, so every workgroup
+// builds the same list.  The lone rows' blocks are then cut into the equal
+// static shares of the resident workers, as in decode_stream_kernel, and
+// the merge kernel combines the split segments.  With more lone rows than
+// the list holds, each wavefront instead claims batches of 64 rows from the
+// claim counter and computes every lone row of a batch whole (no split,
+// nothing to merge; with that many rows the claims balance the load).
+// Workgroup 0 writes the zeros of lone rows without keys and the total the
+// merge kernel schedules from (0 in the claiming mode).
+constexpr int kFusedLone = 2048;
+constexpr int kFusedScanPer = 16;  // rows per thread per scan pass
+
+struct FusedDecodeLds {
+  int64_t cum[kFusedLone + 1];
+  int64_t len[kFusedLone];
+  int32_t seq[kFusedLone];
+  int32_t row[kFusedLone];
+  int64_t wave_sums[2][kWorkersPerGroup];
+  int64_t totals[2];
+  int64_t one_cum[kWorkersPerGroup][2];  // claiming mode: a one-row list per wavefront
+  int64_t one_len[kWorkersPerGroup];
+  int32_t one_seq[kWorkersPerGroup];
+  int32_t one_row[kWorkersPerGroup];
+  int64_t batch_len[kWorkersPerGroup][kWave];  // claiming mode: keys of the batch's rows
+};
+
+// The claiming mode of fused_decode_body: batches of 64 rows from the claim
+// counter, each lone row of a batch computed whole on a one-row list.
+template <int DT, int HD, int TPP, int PF, bool KV8, typename LoneRow>
+__device__ __forceinline__ void fused_claim_rows(const DecodeParams& p, FusedDecodeLds& L,
+                                                          const LoneRow& lone_row) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) p.hdr[0] = 0;  // nothing to merge
+  const int64_t n_rows = p.num_seqs;
+  const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
+  const int wv = wave_id();
+  const int lane = lane_id();
+  for (;;) {
+    uint32_t k = 0;
+    if (lane == 0) k = atomicAdd(p.claim, 1u);
+    const int64_t batch = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(k)) * kWave;
+    if (batch >= n_rows) break;
+    const int64_t r = batch + lane;
+    int64_t len = 0;
+    bool keep = false;
+    if (r < n_rows) {
+      const uint32_t prev = r > 0 ? p.q2seq[r - 1] : 0xFFFFFFFFu;
+      const uint32_t next = r + 1 < n_rows ? p.q2seq[r + 1] : 0xFFFFFFFFu;
+      keep = lone_row(r, prev, p.q2seq[r], next, len);
+    }
+    L.batch_len[wv][lane] = len;
+    uint64_t bits = __ballot(keep);
+    while (bits) {
+      const int j = __builtin_ctzll(bits);
+      bits &= bits - 1;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int64_t lj = L.batch_len[wv][j];
+      if (lane == 0) {
+        L.one_cum[wv][0] = 0;
+        L.one_cum[wv][1] = ((lj + 15) >> 4) * segs;
+        L.one_len[wv] = lj;
+        L.one_seq[wv] = static_cast<int32_t>(p.q2seq[batch + j]);
+        L.one_row[wv] = static_cast<int32_t>(batch + j);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const Sched sc = make_sched(((lj + 15) >> 4) * segs, 1, 0);
+      process_range<DT, HD, TPP, PF, false, KV8>(p, sc, L.one_cum[wv],
+                                                 ItemLds{&L.one_len[wv], &L.one_seq[wv], &L.one_row[wv]}, 1, 0, 1);
+      // every lane is done with this row's list before the next one is written
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+}
+
+template <int DT, int HD, int TPP, int PF, bool KV8>
+__device__ __forceinline__ void fused_decode_body(const DecodeParams& p, FusedDecodeLds& L) {
+  const int tid = threadIdx.x;
+  const int64_t n_rows = p.num_seqs;  // row mode: one item per query row
+  const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
+  const int64_t max_tokens = p.page_table_width * TPP;
+  // a row's sequence, keys and whether it is a lone row with keys
+  auto lone_row = [&](int64_t r, uint32_t prev, uint32_t sq, uint32_t next, int64_t& len) {
+    len = 0;
+    if ((r > 0 && prev == sq) || (r + 1 < n_rows && next == sq)) return false;  // a prefill row
+    if (sq < p.num_pt_rows) {
+      const int64_t l = p.seq_lens[sq];
+      const int64_t off = p.q_offset[r];
+      len = off < l ? off : l;
+      PAL_DEBUG_FLAG(len > max_tokens, kDebugLength);
+      len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
+    }
+    if (len == 0 && blockIdx.x == 0) zero_item_output<HD>(p, r);  // no key: zeros, once
+    return len > 0;
+  };
+
+  int64_t n_lone = 0, n_blocks = 0;  // running totals (uniform)
+  for (int64_t base = 0; base < n_rows; base += static_cast<int64_t>(kGroupThreads) * kFusedScanPer) {
+    const int64_t r0 = base + static_cast<int64_t>(tid) * kFusedScanPer;
+    uint32_t sq[kFusedScanPer + 2];  // q2seq of rows r0 - 1 .. r0 + kFusedScanPer
+#pragma unroll
+    for (int k = 0; k < kFusedScanPer + 2; ++k) {
+      const int64_t r = r0 - 1 + k;
+      sq[k] = (r >= 0 && r < n_rows) ? p.q2seq[r] : 0xFFFFFFFFu;
+    }
+    int64_t lens[kFusedScanPer];
+    int64_t cnt = 0, blk = 0;
+#pragma unroll
+    for (int k = 0; k < kFusedScanPer; ++k) {
+      const int64_t r = r0 + k;
+      lens[k] = 0;
+      if (r < n_rows && lone_row(r, sq[k], sq[k + 1], sq[k + 2], lens[k])) {
+        cnt += 1;
+        blk += ((lens[k] + 15) >> 4) * segs;
+      }
+    }
+    const int64_t inc_c = block_inclusive_scan<kGroupThreads>(cnt, L.wave_sums[0]);
+    const int64_t inc_b = block_inclusive_scan<kGroupThreads>(blk, L.wave_sums[1]);
+    int64_t ci = n_lone + inc_c - cnt, bi = n_blocks + inc_b - blk;
+#pragma unroll
+    for (int k = 0; k < kFusedScanPer; ++k) {
+      if (lens[k] > 0) {
+        if (ci < kFusedLone) {
+          L.cum[ci] = bi;
+          L.len[ci] = lens[k];
+          L.seq[ci] = static_cast<int32_t>(sq[k + 1]);
+          L.row[ci] = static_cast<int32_t>(r0 + k);
+        }
+        ci += 1;
+        bi += ((lens[k] + 15) >> 4) * segs;
+      }
+    }
+    if (tid == kGroupThreads - 1) {
+      L.totals[0] = inc_c;
+      L.totals[1] = inc_b;
+    }
+    __syncthreads();
+    n_lone += L.totals[0];
+    n_blocks += L.totals[1];
+    __syncthreads();  // totals and wave sums are rewritten by the next pass
+  }
+
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kWorkersPerGroup + wave_id();
+  if (n_lone <= kFusedLone) {
+    if (tid == 0) L.cum[n_lone] = n_blocks;
+    if (blockIdx.x == 0 && tid == 0) p.hdr[0] = n_blocks;  // the merge kernel's schedule
+    __syncthreads();
+    if (n_blocks == 0) return;
+    const ItemLds il{L.len, L.seq, L.row};
+    const Sched sc = make_sched(n_blocks, p.num_workers, 0);
+    if (w < sc.nws) process_range<DT, HD, TPP, PF, false, KV8>(p, sc, L.cum, il, n_lone, w, w + 1);
+    return;
+  }
+  fused_claim_rows<DT, HD, TPP, PF, KV8>(p, L, lone_row);
+}
+
+// The fused mixed batch in one launch (head dims up to 128).  Blocks
+// [0, n_dec) are the decode workers of the lone rows (one workgroup per CU,
+// equal static shares of the rows' KV blocks, as in decode_stream_kernel),
+// the other blocks the prefill tiles of the windows of rows.  The decode
+// blocks have the lowest ids, so the dispatcher places them first: they hold
+// one slot on every CU from the start instead of waiting for tiles to drain
+// (equal static shares started late would end late), and the tiles take the
+// other slot, then both once the decode workers are done.  The two roles
+// share one LDS allocation.
+static_assert(kPfThreads == kGroupThreads, "decode workers and prefill tiles share the workgroup shape");
 template <int DT, int HD, int TPP, bool KV8>
 __global__ __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void decode_shared_cu_kernel(const DecodeParams p) {
-  __shared__ int64_t cum_lds[kInlinePlanSeqs + 1];
-  __shared__ int64_t len_lds[kInlinePlanSeqs];
-  __shared__ int32_t seq_lds[kInlinePlanSeqs];
-  __shared__ int64_t wave_sums[kWorkersPerGroup];
-  stream_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), false, KV8>(p, cum_lds, len_lds, seq_lds, wave_sums);
+void fused_kernel(const DecodeParams dp, const PrefillParams pp, const unsigned n_dec) {
+  __shared__ union {
+    FusedDecodeLds d;
+    PrefillLds<HD> f;
+  } lds;
+  if (blockIdx.x < n_dec)
+    fused_decode_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), KV8>(dp, lds.d);
+  else
+    prefill_block<DT, HD, TPP, KV8>(pp, blockIdx.x - n_dec, lds.f);
 }
 
 // Walks the merge list, slot v for virtual worker v (first block < 0:
@@ -998,35 +1183,13 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
   }
 }
 
-template <int DT, int HD, int TPP, bool KV8>
-hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t stream) {
-  hipError_t err;
-  if (p.num_seqs > kInlinePlanSeqs) {
-    hipLaunchKernelGGL((decode_plan_kernel<HD, TPP>), dim3(1), dim3(kPlanThreads), 0, stream, p);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
-  const int64_t groups = (static_cast<int64_t>(p.num_workers) + kWorkersPerGroup - 1) / kWorkersPerGroup;
-  bool plain = true;
-  if constexpr (shares_cu(HD)) {
-    if (shared_cu) {
-      hipLaunchKernelGGL((decode_shared_cu_kernel<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(groups)),
-                         dim3(kGroupThreads), 0, stream, p);
-      plain = false;
-    }
-  }
-  if (plain && p.tokens_per_worker > 0)
-    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, true, KV8>), dim3(static_cast<unsigned>(groups)),
-                       dim3(kGroupThreads), 0, stream, p);
-  else if (plain)
-    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, false, KV8>), dim3(static_cast<unsigned>(groups)),
-                       dim3(kGroupThreads), 0, stream, p);
-  err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  // Live merge slots: one per static share (at most num_workers) with equal
-  // shares, up to list_cap in the fixed-chunk mode.  A workgroup with no
-  // live slot still pays one fetch round trip, so the equal-share grid is
-  // not padded beyond the workers (it then fits the GPU in one round).
+// The merge of split segments, after the stream kernel.  Live merge slots:
+// one per static share (at most num_workers) with equal shares, up to
+// list_cap in the fixed-chunk mode.  A workgroup with no live slot still pays
+// one fetch round trip, so the equal-share grid is not padded beyond the
+// workers (it then fits the GPU in one round).
+template <int DT, int HD, int TPP>
+hipError_t launch_merge(const DecodeParams& p, hipStream_t stream) {
   const bool all_static = p.tokens_per_worker == 0 && kStaticShareNum == kStaticShareDen;
   int64_t merge_groups = all_static ? p.num_workers : kMergeGroups;
   if (merge_groups > p.list_cap) merge_groups = p.list_cap;
@@ -1035,32 +1198,106 @@ hipError_t launch_decode_t(const DecodeParams& p, bool shared_cu, hipStream_t st
   return hipGetLastError();
 }
 
+// The scan of batches above kInlinePlanSeqs items, before the stream kernel.
+template <int HD, int TPP>
+hipError_t launch_plan(const DecodeParams& p, hipStream_t stream) {
+  if (p.num_seqs <= kInlinePlanSeqs) return hipSuccess;
+  hipLaunchKernelGGL((decode_plan_kernel<HD, TPP>), dim3(1), dim3(kPlanThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int DT, int HD, int TPP, bool KV8>
+hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+  hipError_t err = launch_plan<HD, TPP>(p, stream);
+  if (err != hipSuccess) return err;
+  const int64_t groups = (static_cast<int64_t>(p.num_workers) + kWorkersPerGroup - 1) / kWorkersPerGroup;
+  if (p.tokens_per_worker > 0)
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, true, KV8>), dim3(static_cast<unsigned>(groups)),
+                       dim3(kGroupThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_stream_kernel<DT, HD, TPP, false, KV8>), dim3(static_cast<unsigned>(groups)),
+                       dim3(kGroupThreads), 0, stream, p);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  return launch_merge<DT, HD, TPP>(p, stream);
+}
+
 template <int DT, int HD, bool KV8>
-hipError_t dispatch_tpp(const DecodeParams& p, int tpp, bool shared_cu, hipStream_t stream) {
+hipError_t dispatch_tpp(const DecodeParams& p, int tpp, hipStream_t stream) {
   switch (tpp) {
-    case 16: return launch_decode_t<DT, HD, 16, KV8>(p, shared_cu, stream);
-    case 32: return launch_decode_t<DT, HD, 32, KV8>(p, shared_cu, stream);
+    case 16: return launch_decode_t<DT, HD, 16, KV8>(p, stream);
+    case 32: return launch_decode_t<DT, HD, 32, KV8>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int DT>
-hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, bool shared_cu, bool kv8, hipStream_t stream) {
+hipError_t dispatch_hd(const DecodeParams& p, int hd, int tpp, bool kv8, hipStream_t stream) {
   if (kv8) {  // fp8 pools: head dims that are whole 64-dim stripe rounds
     switch (hd) {
-      case 64: return dispatch_tpp<DT, 64, true>(p, tpp, shared_cu, stream);
-      case 128: return dispatch_tpp<DT, 128, true>(p, tpp, shared_cu, stream);
-      case 256: return dispatch_tpp<DT, 256, true>(p, tpp, shared_cu, stream);
+      case 64: return dispatch_tpp<DT, 64, true>(p, tpp, stream);
+      case 128: return dispatch_tpp<DT, 128, true>(p, tpp, stream);
+      case 256: return dispatch_tpp<DT, 256, true>(p, tpp, stream);
       default: return hipErrorInvalidValue;
     }
   }
   switch (hd) {
-    case 32: return dispatch_tpp<DT, 32, false>(p, tpp, shared_cu, stream);
-    case 64: return dispatch_tpp<DT, 64, false>(p, tpp, shared_cu, stream);
-    case 80: return dispatch_tpp<DT, 80, false>(p, tpp, shared_cu, stream);
-    case 96: return dispatch_tpp<DT, 96, false>(p, tpp, shared_cu, stream);
-    case 128: return dispatch_tpp<DT, 128, false>(p, tpp, shared_cu, stream);
-    case 256: return dispatch_tpp<DT, 256, false>(p, tpp, shared_cu, stream);
+    case 32: return dispatch_tpp<DT, 32, false>(p, tpp, stream);
+    case 64: return dispatch_tpp<DT, 64, false>(p, tpp, stream);
+    case 80: return dispatch_tpp<DT, 80, false>(p, tpp, stream);
+    case 96: return dispatch_tpp<DT, 96, false>(p, tpp, stream);
+    case 128: return dispatch_tpp<DT, 128, false>(p, tpp, stream);
+    case 256: return dispatch_tpp<DT, 256, false>(p, tpp, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// The fused op: the fused kernel, then the merge; head dims above 128: the
+// decode rows' kernels, then the prefill tiles.
+template <int DT, int HD, int TPP, bool KV8>
+hipError_t launch_fused_t(const DecodeParams& dp, const PrefillParams& pp, hipStream_t stream) {
+  if constexpr (shares_cu(HD)) {
+    hipError_t err;
+    const int64_t n_dec = (static_cast<int64_t>(dp.num_workers) + kWorkersPerGroup - 1) / kWorkersPerGroup;
+    const int64_t n_pf = static_cast<int64_t>(pp.num_units) * pp.num_kv_heads * pp.head_chunks;
+    if (n_dec + n_pf > 0x7FFFFFFFll) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((fused_kernel<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(n_dec + n_pf)),
+                       dim3(kGroupThreads), 0, stream, dp, pp, static_cast<unsigned>(n_dec));
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_merge<DT, HD, TPP>(dp, stream);
+  } else {
+    const hipError_t err = launch_decode_t<DT, HD, TPP, KV8>(dp, stream);
+    if (err != hipSuccess) return err;
+    return launch_prefill(pp, DT, HD, TPP, stream);
+  }
+}
+
+template <int DT, int HD, bool KV8>
+hipError_t fused_tpp(const DecodeParams& dp, const PrefillParams& pp, int tpp, hipStream_t stream) {
+  switch (tpp) {
+    case 16: return launch_fused_t<DT, HD, 16, KV8>(dp, pp, stream);
+    case 32: return launch_fused_t<DT, HD, 32, KV8>(dp, pp, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int DT>
+hipError_t fused_hd(const DecodeParams& dp, const PrefillParams& pp, int hd, int tpp, bool kv8, hipStream_t stream) {
+  if (kv8) {
+    switch (hd) {
+      case 64: return fused_tpp<DT, 64, true>(dp, pp, tpp, stream);
+      case 128: return fused_tpp<DT, 128, true>(dp, pp, tpp, stream);
+      case 256: return fused_tpp<DT, 256, true>(dp, pp, tpp, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (hd) {
+    case 32: return fused_tpp<DT, 32, false>(dp, pp, tpp, stream);
+    case 64: return fused_tpp<DT, 64, false>(dp, pp, tpp, stream);
+    case 96: return fused_tpp<DT, 96, false>(dp, pp, tpp, stream);
+    case 128: return fused_tpp<DT, 128, false>(dp, pp, tpp, stream);
+    case 256: return fused_tpp<DT, 256, false>(dp, pp, tpp, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1153,11 +1390,19 @@ int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partiti
   return 5 * resident + 1;  // static shares plus about four claimed chunks per worker
 }
 
-hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
-                         hipStream_t stream) {
+hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream) {
   const bool kv8 = p.k_scales != nullptr;
-  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, shared_cu, kv8, stream);
-  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, shared_cu, kv8, stream);
+  if (dtype == kBF16) return dispatch_hd<kBF16>(p, head_dim, tokens_per_page, kv8, stream);
+  return dispatch_hd<kF16>(p, head_dim, tokens_per_page, kv8, stream);
+}
+
+bool fused_shares_cu(int head_dim) { return shares_cu(head_dim); }
+
+hipError_t launch_fused(const DecodeParams& dp, const PrefillParams& pp, int dtype, int head_dim, int tokens_per_page,
+                        hipStream_t stream) {
+  const bool kv8 = dp.k_scales != nullptr;
+  if (dtype == kBF16) return fused_hd<kBF16>(dp, pp, head_dim, tokens_per_page, kv8, stream);
+  return fused_hd<kF16>(dp, pp, head_dim, tokens_per_page, kv8, stream);
 }
 
 }  // namespace pal

@@ -3,15 +3,14 @@
 // Replaces the reference's binding + primitive host layers
 // (src/pal_core/bindings.cpp, src/pal_core/src/ops.cpp,
 // src/pal_core/src/*_primitive.cpp).  The library keeps a thread-local error
-// message and, per device, the fused op's side stream and its two events; it
-// never allocates device memory.
+// message, a cache of occupancy-derived worker counts and, per device, the
+// scratch array of the no-allocation entry point; it never allocates device
+// memory.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
-#include <map>
-#include <mutex>
 #include <string>
 
 #include "../../include/pal_hip.h"
@@ -108,32 +107,6 @@ int decode_workers(int dtype, int head_dim, int tokens_per_page, int64_t num_seq
   *resident = res;
   *virtual_workers = vw;
   return PAL_OK;
-}
-
-// Side stream of the fused op, one per device: the prefill tiles (MFMA-bound)
-// run on it while the decode rows (HBM-bound) run on the caller's stream, so
-// the two halves of a mixed batch overlap.  Fork and join are event waits,
-// which stream capture records like any other dependency.  Default priority.
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t join = nullptr;
-};
-std::mutex g_side_mu;
-std::map<int, SideStream> g_side;
-
-hipError_t side_stream(int device, SideStream** out) {
-  SideStream& ss = g_side[device];
-  if (!ss.stream) {
-    hipError_t err = hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking);
-    if (err != hipSuccess) return err;
-    err = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming);
-    if (err != hipSuccess) return err;
-    err = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming);
-    if (err != hipSuccess) return err;
-  }
-  *out = &ss;
-  return hipSuccess;
 }
 
 // Common decode parameter set-up (plain decode: item i = row i = sequence i).
@@ -394,7 +367,7 @@ size_t fused_workspace_size(int dtype, int64_t num_query_rows, int num_q_heads, 
   int resident = 0;
   int64_t vw = 0;
   if (decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, (group + 15) / 16, 0, 0,
-                     true, kv8, &resident, &vw) != PAL_OK)
+                     pal::fused_shares_cu(head_dim), kv8, &resident, &vw) != PAL_OK)
     return 0;
   return decode_layout(num_query_rows, head_dim, group < 16 ? group : 16, vw).total;
 }
@@ -429,9 +402,8 @@ int fused_call(const void* queries, const void* k_pool, const void* v_pool, cons
   const int chunks = (group + 15) / 16;
   int resident = 0;
   int64_t vw = 0;
-  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0, true, kv8,
-                      &resident,
-                      &vw);
+  st = decode_workers(dtype, head_dim, tokens_per_page, num_query_rows, num_kv_heads, chunks, 0, 0,
+                      pal::fused_shares_cu(head_dim), kv8, &resident, &vw);
   if (st != PAL_OK) return st;
   const DecodeLayout lay = decode_layout(num_query_rows, head_dim, hg_max, vw);
   if (workspace == nullptr || workspace_bytes < lay.total)
@@ -485,27 +457,7 @@ int fused_call(const void* queries, const void* k_pool, const void* v_pool, cons
           op, static_cast<long long>(num_query_rows), static_cast<long long>(num_seqs), num_q_heads, num_kv_heads,
           head_dim, tokens_per_page, dtype, kv8 ? 1 : 0, static_cast<long long>(windows), resident,
           static_cast<void*>(hs));
-  // The decode grid (one persistent workgroup per CU) is launched first on
-  // the caller's stream, then the prefill tiles on the side stream fill the
-  // remaining slots; the caller's stream waits for both.
-  int dev = 0;
-  hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) return hip_status(err, op);
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  SideStream* ss = nullptr;
-  err = side_stream(dev, &ss);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = hipEventRecord(ss->fork, hs);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = hipStreamWaitEvent(ss->stream, ss->fork, 0);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = pal::launch_decode(dp, dtype, head_dim, tokens_per_page, true, hs);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = pal::launch_prefill(pp, dtype, head_dim, tokens_per_page, ss->stream);
-  if (err != hipSuccess) return hip_status(err, op);
-  err = hipEventRecord(ss->join, ss->stream);
-  if (err != hipSuccess) return hip_status(err, op);
-  return hip_status(hipStreamWaitEvent(hs, ss->join, 0), op);
+  return hip_status(pal::launch_fused(dp, pp, dtype, head_dim, tokens_per_page, hs), op);
 }
 
 // pal_paged_attention_decode and its no-allocation variant: with
@@ -586,7 +538,7 @@ int decode_call(const void* queries, const void* k_pool, const void* v_pool, con
           static_cast<long long>(num_seqs), num_q_heads, num_kv_heads, head_dim, tokens_per_page,
           static_cast<long long>(page_table_width), dtype, kv8 ? 1 : 0, partition_size, resident,
           static_cast<long long>(vw), lay.total, use_scratch ? 1 : 0, static_cast<void*>(stream));
-  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, false, stream),
+  return hip_status(pal::launch_decode(p, dtype, head_dim, tokens_per_page, stream),
                     "paged_attention_decode");
 }
 

@@ -99,6 +99,11 @@ struct Dt<kBF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // acc + lo + hi of a packed pair (one v_dot2c_f32_bf16 against (1, 1))
+  static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                           acc, false);
+  }
   // two fp8 e4m3 values (bytes 0-1, or 2-3 when hi) of w as a packed pair;
   // exact: every e4m3 value is a bf16 value
   static __device__ __forceinline__ uint32_t fp8x2(uint32_t w, bool hi) {
@@ -131,6 +136,10 @@ struct Dt<kF16> {
   static __device__ __forceinline__ f32x16 mma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // acc + lo + hi of a packed pair (one v_dot2c_f32_f16 against (1, 1))
+  static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
   }
   // two fp8 e4m3 values as a packed pair; exact (e4m3's range and 3-bit
   // mantissa fit fp16, subnormals included)
@@ -165,13 +174,16 @@ constexpr int kLgkmZero = 15 | (3 << 14) | (7 << 4);
 // Issued as inline assembly so that the compiler does not track an LDS write
 // in flight: it would otherwise wait for every such copy (vmcnt(0)) before
 // later LDS reads it cannot prove disjoint.  Callers wait with counted
-// s_waitcnt.  The s_nop keeps the one wait state between the M0 write and
-// the copy.
+// s_waitcnt.  The compiler's hazard pass does not look inside the asm, so
+// the asm carries the wait states itself: s_nop 4 gives the five that a
+// vector memory instruction needs after a VALU write of an SGPR it reads (the
+// compiler may materialise the base with v_readlane / v_readfirstlane right
+// before the asm), which also covers the one after the M0 write.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));  // low half of a generic LDS address
 }
 __device__ __forceinline__ void copy_to_lds16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // Scheduling fence: the compiler's instruction scheduler moves nothing
@@ -188,10 +200,14 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
-// max / sum of v and its value in lane l ^ 32 (v_permlane32_swap: no LDS trip)
+// max / sum of v and its value in lane l ^ 32 (v_permlane32_swap: no LDS trip).
+// The max is one plain v_max_f32: the scores it compares are finite or
+// -inf, so the NaN quieting fmaxf would add is not needed.
 __device__ __forceinline__ float max_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  return m;
 }
 __device__ __forceinline__ float sum_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -91,16 +91,16 @@ struct DecodeParams {
 };
 
 // Workers the GPU keeps resident for this kernel configuration (shared_cu:
-// the fused op's decode, one workgroup per CU beside the prefill tiles;
-// chunks: the fixed-chunk mode, partition_size > 0; kv8: fp8 pools).
+// the fused kernel's decode workers, one workgroup per CU beside the prefill
+// tiles, head dims up to 128; chunks: the fixed-chunk mode,
+// partition_size > 0; kv8: fp8 pools).
 hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page, bool shared_cu, bool chunks,
                                    bool kv8, int* workers);
 // Virtual workers (merge-list and partial slots) a call can produce: the
 // resident workers' equal shares, or, with a partition size, one per fixed
 // chunk of max_blocks (the 16-token blocks the page tables can hold).
 int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partition_size);
-hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, bool shared_cu,
-                         hipStream_t stream);
+hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
 
 // Causal attention over query tiles (prefill rows).  Uniform-prompt mode
 // (prompt_len > 0): the reference prefill, keys past each sequence's history
@@ -138,6 +138,13 @@ struct PrefillParams {
 // Query tokens per prefill tile (and window) for a GQA group size.
 int prefill_tokens_per_tile(int group);
 hipError_t launch_prefill(const PrefillParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream);
+
+// The fused mixed batch: the decode rows (dp, row mode) and the prefill tiles
+// (pp, window mode) in one kernel for head dims up to 128 (then dp's workers
+// are one workgroup per CU: fused_shares_cu), one after the other above.
+bool fused_shares_cu(int head_dim);
+hipError_t launch_fused(const DecodeParams& dp, const PrefillParams& pp, int dtype, int head_dim, int tokens_per_page,
+                        hipStream_t stream);
 
 // Page moves of a compaction: pages src[m] -> dst[m] of both pools (whole
 // pages, page_bytes each) and, for fp8 pools, their scale rows.  Sources and

@@ -1,44 +1,11 @@
-// Paged causal attention for query tiles (prefill and the prefill rows of the
-// fused mixed batch) on gfx950 MFMA.
+// Paged causal attention for query tiles on gfx950 MFMA: the prefill kernel
+// (the reference's uniform-prompt signature) and the prefill half of the
+// fused mixed batch.  The tile code and its design notes are in
+// prefill_tile.h.
 //
 // Reference behaviour: kernels/paged_attention/prefill/paged_attention_prefill.h.metal
-// -- a prompt token attends to the cached history and to prompt tokens at or
-// before it (:147-234, :251-360), scores scaled by 1/sqrt(HD) after the dot
-// product (:178, :302), output rows (token, head) (:379-381).  In the fused
-// op every key is read from pages: row r of sequence s sees keys
-// [0, min(len[s], q_offset[r])), which is exactly the causal mask when the
-// new tokens were written to the pages first.
-//
-// Design (MI355X):
-//  * One workgroup (4 wavefronts) owns a tile of 128 "M-rows": QT consecutive
-//    query tokens of one sequence times the (up to 16) query heads sharing a
-//    kv head, so one K/V tile in LDS serves the whole GQA group.
-//  * Per 32-key step the K and V tiles reach LDS by direct-to-LDS copies
-//    (global_load_lds_dwordx4, no registers), issued two steps ahead into four
-//    LDS buffers, with counted waits and one barrier per step.  Page ids come
-//    from an LDS copy of the tile's page-table slice.  Steps at the tile end
-//    or with dense prompt keys take a synchronous register path.
-//  * Each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
-//    from LDS, B = Q^T held in registers) and O^T += V^T * P^T with the same
-//    instruction.  In the transposed products a lane owns one M-row, so the
-//    softmax max / sum need one cross-half exchange (v_permlane32_swap) and
-//    the probabilities go into the PV MFMA without leaving the lane.  K is
-//    stored in the QK operand's row order and V rows are swizzled, so every
-//    operand read is one conflict-free 16-byte LDS access.
-//  * Steps are software-pipelined inside a wavefront: the QK MFMAs of step
-//    st+1 are issued among the exponentials of step st.
-//  * Online softmax in log2 units with a lazy rescale: the running max is only
-//    moved when a score exceeds it by more than 2^8, so O is rescaled rarely.
-//  * Causal skipping: the key loop stops at the tile's largest limit, and key
-//    steps below every row's limit skip the mask arithmetic.
-//  * Two ways to name the work, both without a planning pass: the reference
-//    prefill's uniform prompt (S sequences x P prompt rows; tiles are pure
-//    arithmetic; keys [0, hist[s]) come from pages and keys hist[s] + i from
-//    the dense prompt K/V rows s*P + i, as prefill.h.metal:147-234 reads
-//    them), or windows of consecutive query rows (the fused op), each run of
-//    rows of one sequence in a window being a tile.
-#include <type_traits>
-
+// (history + causal prompt keys :147-234, :251-360; scores scaled after the
+// dot product :178, :302; output rows (token, head) :379-381).
 #include "pal_device.h"
 
 namespace pal {
@@ -46,579 +13,19 @@ namespace pal {
 // flag word of this translation unit's debug checks (see pal_device.h)
 PAL_DEBUG_FLAGS_DEFINE(prefill_debug_flags)
 
+}  // namespace pal
+
+#include "prefill_tile.h"
+
+namespace pal {
+
 namespace {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kMRows = kPfWaves * 32;  // M-rows (token, head) per workgroup
-constexpr int kKeys = 32;              // keys per step
-constexpr int kNBuf = 4;               // LDS step buffers (read by stragglers, computed, two in flight)
-constexpr int kPidChunk = 512;         // page ids staged per chunk; two chunks live in LDS
-constexpr float kLazyRescale = 8.f;    // log2 headroom before the running max moves
-
-// A step moves 4*HD items of 16 bytes of K and as many of V.
-template <int HD>
-struct StepGeo {
-  static constexpr int kItems = 4 * HD;
-  static constexpr int kLoads = (kItems + kPfThreads - 1) / kPfThreads;  // per thread, per K (or V)
-};
-
-// Item <-> (page, offset) maps.  LDS holds each step's items in item order,
-// so one direct-to-LDS load per wavefront fills 1 KiB of consecutive slots
-// (lane l -> slot base + l).  With TPP 16 the items are page-major (2*HD per
-// page), which also makes each load instruction read a single page.
-//   K item i: stripe c, slot t of the step holds key kperm(t):  page offset (c*TPP + kperm(t) % TPP) * 8
-//   V item i: row d, 8-key group g' = g ^ swz(d) of the row:     page offset d*TPP + 8 g'
-// K keys are stored in the QK operand's row order (kperm, an involution
-// swapping bits 2 and 3 of the key index), so the operand reads are
-// contiguous; the V groups are swizzled by row so that the PV operand reads
-// (one 16-byte chunk per lane and row) spread over all banks.
-__device__ __forceinline__ int kperm(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
-
-template <int HD, int TPP>
-struct ItemMap {
-  static __device__ __forceinline__ int k_page_half(int i) { return TPP == 16 ? i / (2 * HD) : 0; }
-  // K item i: stripe c and the key (within the step) it carries
-  static __device__ __forceinline__ void k_item(int i, int& c, int& key) {
-    if (TPP == 16) {
-      const int rem = i % (2 * HD);
-      c = rem / 16;
-      key = (i / (2 * HD)) * 16 + kperm(rem % 16);
-    } else {
-      c = i / 32;
-      key = kperm(i % 32);
-    }
-  }
-  static __device__ __forceinline__ int k_offset(int i) {  // element offset inside the (page, kv head) block
-    int c, key;
-    k_item(i, c, key);
-    return (c * TPP + key % TPP) * 8;
-  }
-  // Conflict-free for 8-lane groups over 32 banks and 16-lane groups over 64
-  // banks: within any 8 (and any 16) consecutive rows the 16-byte chunk each
-  // lane reads lands on a distinct bank group.
-  static __device__ __forceinline__ int v_swz(int d) {
-    return TPP == 16 ? ((d >> 2) ^ (d >> 3)) & 1 : ((d >> 1) ^ (d >> 3)) & 3;
-  }
-  // V item i: row d and the group g stored in its slot (key offset in the step)
-  static __device__ __forceinline__ void v_item(int i, int& d, int& key) {
-    if (TPP == 16) {
-      const int rem = i % (2 * HD);
-      d = rem / 2;
-      key = (i / (2 * HD)) * 16 + 8 * ((rem % 2) ^ v_swz(d));
-    } else {
-      d = i / 4;
-      key = 8 * ((i % 4) ^ v_swz(d));
-    }
-  }
-  // LDS slot of K operand row m (key kperm(m) of the step), stripe c
-  static __device__ __forceinline__ int k_slot(int m, int c) {
-    return TPP == 16 ? (m / 16) * (2 * HD) + c * 16 + m % 16 : c * 32 + m;
-  }
-  // LDS slot holding V row d, keys kg .. kg+7 of the step (kg multiple of 8)
-  static __device__ __forceinline__ int v_slot(int d, int kg) {
-    return TPP == 16 ? (kg / 16) * (2 * HD) + d * 2 + (((kg / 8) % 2) ^ v_swz(d)) : d * 4 + ((kg / 8) ^ v_swz(d));
-  }
-  // v_slot(d + 32 n, kg) - v_slot(d, kg): v_swz depends on bits 1..3 of d only
-  static constexpr int kVRowTile = TPP == 16 ? 64 : 128;
-};
-
-// One query tile: rows [row0, row0 + nrows) of sequence s (nrows <= tokens
-// per tile), query heads h0 .. h0+15 of kv head kvh.  PROMPT: the
-// uniform-prompt mode (keys below the history length from pages, the rest
-// from the dense prompt rows of sequence s); otherwise every key from pages.
-template <int DT, int HD, int TPP, bool PROMPT, bool KV8>
-__device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, int nrows, int64_t s, int kvh, int h0,
-                                             uint16_t* k_lds_base, uint16_t* v_lds_base, uint16_t* junk_lds,
-                                             uint32_t* pid_lds, int* lim_lds) {
-  static_assert(HD % 32 == 0, "prefill needs head_dim % 32 == 0");
-  constexpr int KS = HD / 16;  // QK k-steps of 16
-  constexpr int DT32 = HD / 32;  // O^T row tiles of 32 dims
-  constexpr int NI = StepGeo<HD>::kItems;
-  constexpr int NL = StepGeo<HD>::kLoads;
-  using IM = ItemMap<HD, TPP>;
-  auto k_lds = [&](int b) { return k_lds_base + b * NI * 8; };
-  auto v_lds = [&](int b) { return v_lds_base + b * NI * 8; };
-
-  // tile coordinates are workgroup-uniform: keep them in scalar registers
-  row0 = __builtin_amdgcn_readfirstlane(row0);
-  nrows = __builtin_amdgcn_readfirstlane(nrows);
-  s = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(s)));
-  const int hg = min(16, p.group - h0);  // heads of this chunk
-  const int qt = kMRows / p.hg_max;      // tokens per tile (hg_max = min(group, 16))
-  constexpr bool prompt_mode = PROMPT;
-  const bool seq_ok = s < p.num_seqs;  // a row naming no sequence attends to nothing
-  if (!seq_ok) s = 0;
-  const int tid = threadIdx.x;
-  const int lane = lane_id();
-  const int w = wave_id();
-  const int col = lane & 31;  // this lane's M-row within the wave
-  const int half = lane >> 5;
-
-  const int64_t max_tokens = p.page_table_width * TPP;
-  int64_t hist = 0;  // prompt mode: keys below hist come from pages
-  int64_t slen;
-  if (prompt_mode) {
-    hist = p.seq_lens[s];
-    PAL_DEBUG_FLAG(hist > max_tokens, kDebugLength);
-    hist = hist < 0 ? 0 : (hist > max_tokens ? max_tokens : hist);
-    slen = hist + p.prompt_len;
-  } else {
-    slen = seq_ok ? p.seq_lens[s] : 0;
-    PAL_DEBUG_FLAG(slen > max_tokens, kDebugLength);
-    slen = slen < 0 ? 0 : (slen > max_tokens ? max_tokens : slen);
-  }
-
-  // Row limits: M-row m = token * hg_max + head.
-  __syncthreads();  // the previous tile is done with every LDS array
-  if (tid < kMRows) {
-    const int t = tid / p.hg_max;
-    const int hh = tid % p.hg_max;
-    int lim = 0;
-    if (t < nrows && t < qt && hh < hg) {
-      int64_t off = prompt_mode ? hist + (row0 + t - s * p.prompt_len) + 1 : p.q_offset[row0 + t];
-      off = off < 0 ? 0 : off;
-      lim = static_cast<int>(off < slen ? off : slen);
-    }
-    lim_lds[tid] = lim;
-  }
-  __syncthreads();
-  int max_lim = 0, min_lim = 1 << 30;
-  for (int i = 0; i < kMRows; ++i) {  // uniform LDS broadcast reads
-    const int t = i / p.hg_max;
-    const int hh = i % p.hg_max;
-    if (t < nrows && t < qt && hh < hg) {
-      max_lim = max(max_lim, lim_lds[i]);
-      min_lim = min(min_lim, lim_lds[i]);
-    }
-  }
-  max_lim = __builtin_amdgcn_readfirstlane(max_lim);
-  min_lim = __builtin_amdgcn_readfirstlane(min_lim);
-  const int m_row = w * 32 + col;  // this lane's M-row
-  const int my_t = m_row / p.hg_max;
-  const int my_h = m_row % p.hg_max;
-  const bool row_ok = my_t < nrows && my_t < qt && my_h < hg;
-  const int my_lim = lim_lds[m_row];
-
-  // Q^T operand: lane holds Q[M-row col][16kk + 8 half .. +7] for all k-steps.
-  u32x4 qv[KS];
-  {
-    const int64_t qrow = static_cast<int64_t>(row0 + (row_ok ? my_t : 0)) * p.num_q_heads + kvh * p.group + h0 +
-                         (row_ok ? my_h : 0);
-    const uint16_t* qp = p.q + qrow * HD + 8 * half;
-    const uint32_t qmask = row_ok ? 0xFFFFFFFFu : 0u;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qv[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk) & qmask;
-  }
-
-  const int64_t head_block = static_cast<int64_t>(HD) * TPP;
-  const int64_t page_stride = head_block * p.num_kv_heads;
-  const int64_t page_stride8 = page_stride;            // fp8 pools: bytes per page (one byte per element)
-  const int64_t kv_head_off8 = kvh * head_block;       // and of a kv head's block
-  const uint32_t* pt = p.page_table + s * p.page_table_width;
-  const int64_t dense_row0 = s * p.prompt_len - hist;  // dense row of key token tok: dense_row0 + tok
-  const int64_t dense_stride = static_cast<int64_t>(p.num_kv_heads) * HD;
-  const int64_t kv_head_off = kvh * head_block;
-  const int nsteps = (max_lim + kKeys - 1) / kKeys;
-  // page-table entries the tile reads: keys below max_lim, and in prompt mode
-  // only those below the history (the rest are dense) -- never past the width
-  const int paged_keys = prompt_mode ? min(max_lim, static_cast<int>(hist)) : max_lim;
-  const int n_pid = (paged_keys + TPP - 1) / TPP;
-
-  // Page ids live in LDS (two chunks of 512 entries, entry e in slot e % 1024):
-  // reading them is an LDS broadcast, so the only vector-memory traffic in the
-  // step loop is the K/V copies, whose count the waits below rely on.
-  auto stage_pids = [&](int chunk) {  // synchronous; callers hold a barrier after it
-    for (int e = chunk * kPidChunk + tid; e < min((chunk + 1) * kPidChunk, n_pid); e += kPfThreads)
-      pid_lds[e % (2 * kPidChunk)] = pt[e];
-  };
-
-  // Fast step: all 32 keys below the tile's largest limit, in valid pages
-  // (and, in prompt mode, below the history): one direct-to-LDS copy per item,
-  // no registers, nothing to wait for here.  Every wavefront issues exactly
-  // 2*NL copies (items past the step go to a junk slot), so the wait counts
-  // are the same on every wavefront.
-  // Slow step (tile end, invalid pages, dense prompt keys): register loads,
-  // masked, then LDS stores -- synchronous, so it also drains the copies in
-  // flight, which keeps the counted waits safe.
-  // pg0 / pg1: the pages of the step's first and (TPP 16) second 16 keys.
-  constexpr bool kAllItems = NI % kPfThreads == 0;  // no wavefront has a padding copy
-  __builtin_assume(w >= 0 && w < kPfWaves);
-  // page ids >= 2^32 - 1 cannot occur with fewer pages; such an id takes the slow path
-  const uint32_t np32 = p.num_pages > 0xFFFFFFFFll ? 0xFFFFFFFFu : static_cast<uint32_t>(p.num_pages);
-  auto issue = [&](int j, uint32_t pg0, uint32_t pg1) {
-    const int buf = j % kNBuf;
-    const int k0 = j * kKeys;
-    if (TPP != 16) pg1 = pg0;
-    // fp8 pools take the register path: the copies cannot dequantize
-    const bool fast = !KV8 && k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 &&
-                      (!prompt_mode || k0 + kKeys <= hist);
-    if (fast) {
-      const int64_t off0 = static_cast<int64_t>(pg0) * page_stride + kv_head_off;
-      const int64_t off1 = static_cast<int64_t>(pg1) * page_stride + kv_head_off;
-#pragma unroll
-      for (int jj = 0; jj < NL; ++jj) {
-        const int i = tid + jj * kPfThreads;
-        const int ib = w * kWave + jj * kPfThreads;  // first item of this wavefront's load
-        const bool ok = kAllItems || ib < NI;
-        const uint16_t* page = p.k_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
-        const uint32_t src = 2u * static_cast<uint32_t>(ok ? IM::k_offset(i) : 0);
-        copy_to_lds16(page, src, lds_addr(ok ? k_lds(buf) + ib * 8 : junk_lds));
-      }
-#pragma unroll
-      for (int jj = 0; jj < NL; ++jj) {
-        const int i = tid + jj * kPfThreads;
-        const int ib = w * kWave + jj * kPfThreads;
-        const bool ok = kAllItems || ib < NI;
-        const uint16_t* page = p.v_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
-        int d = 0, key = 0;
-        if (ok) IM::v_item(i, d, key);
-        const uint32_t src = 2u * static_cast<uint32_t>(d * TPP + key % TPP);
-        copy_to_lds16(page, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
-      }
-      return;
-    }
-#pragma unroll
-    for (int jj = 0; jj < NL; ++jj) {
-      const int i = tid + jj * kPfThreads;
-      if (i >= NI) continue;
-      const uint32_t pg = IM::k_page_half(i) ? pg1 : pg0;
-      const bool pg_ok = pg < p.num_pages;
-      PAL_DEBUG_FLAG(!pg_ok && k0 + (IM::k_page_half(i) ? 16 : 0) < (prompt_mode ? min(max_lim, static_cast<int>(hist)) : max_lim),
-                     kDebugPageId);
-      // K: stripe c, key kj of the step
-      {
-        int kj, c;
-        IM::k_item(i, c, kj);
-        const int tok = k0 + kj;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (!prompt_mode || tok < hist) {
-          if (pg_ok && tok < max_lim) {
-            if constexpr (KV8) {  // dims 8c..8c+7: half of 16-dim stripe c / 2, times the page's K scale
-              const uint8_t* kp8 = reinterpret_cast<const uint8_t*>(p.k_pool) + static_cast<int64_t>(pg) * page_stride8 +
-                                   kv_head_off8 + ((c >> 1) * TPP + kj % TPP) * 16 + (c & 1) * 8;
-              val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(kp8),
-                                     p.k_scales[static_cast<int64_t>(pg) * p.num_kv_heads + kvh]);
-            } else {
-              val = *reinterpret_cast<const u32x4*>(p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off +
-                                                    IM::k_offset(i));
-            }
-          }
-        } else if (tok < max_lim) {
-          val = *reinterpret_cast<const u32x4*>(p.k_dense + (dense_row0 + tok) * dense_stride + kvh * HD + c * 8);
-        }
-        *reinterpret_cast<u32x4*>(k_lds(buf) + i * 8) = val;
-      }
-      // V: row d, keys key .. key+7 of the step
-      {
-        int d, key;
-        IM::v_item(i, d, key);
-        const int tok = k0 + key;
-        const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off + d * TPP;
-        const uint8_t* vpage8 = reinterpret_cast<const uint8_t*>(p.v_pool) + static_cast<int64_t>(pg) * page_stride8 +
-                                kv_head_off8 + d * TPP;
-        const float vsc = KV8 && pg_ok ? p.v_scales[static_cast<int64_t>(pg) * p.num_kv_heads + kvh] : 1.f;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (!prompt_mode || tok + 8 <= hist) {
-          if (pg_ok && tok < max_lim) {
-            if constexpr (KV8) {
-              val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(vpage8 + key % TPP), vsc);
-            } else {
-              val = *reinterpret_cast<const u32x4*>(vpage + key % TPP);
-            }
-          }
-        } else if (tok < max_lim) {
-          // some of the 8 keys are prompt tokens (dense, strided by row)
-          uint32_t e16[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int t2 = tok + e;
-            const bool pgd = t2 < hist;
-            uint16_t x = 0;
-            if (t2 < max_lim && (!pgd || pg_ok)) {
-              if (!pgd) {
-                x = p.v_dense[(dense_row0 + t2) * dense_stride + kvh * HD + d];
-              } else if constexpr (KV8) {
-                const uint32_t code = vpage8[(key + e) % TPP];
-                x = static_cast<uint16_t>(fp8x8_scaled<DT>(u32x2{code, 0u}, vsc)[0] & 0xFFFFu);
-              } else {
-                x = vpage[(key + e) % TPP];
-              }
-            }
-            e16[e] = x;
-          }
-          val = {e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16)};
-        }
-        // keys past the largest limit may hold anything (NaN bits included)
-        const int valid = max_lim - tok;
-        if (valid < 8) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t keep = (2 * e < valid ? 0x0000FFFFu : 0u) | (2 * e + 1 < valid ? 0xFFFF0000u : 0u);
-            val[e] &= keep;
-          }
-        }
-        *reinterpret_cast<u32x4*>(v_lds(buf) + i * 8) = val;
-      }
-    }
-  };
-  // the page ids of step j (an LDS broadcast read; TPP 32: one page)
-  auto read_pids = [&](int j) {
-    const int e = (j * kKeys / TPP) % (2 * kPidChunk);
-    u32x2 v;
-    if (TPP == 16) {
-      v = *reinterpret_cast<const u32x2*>(pid_lds + e);  // e is even: 8-byte aligned
-    } else {
-      v.x = pid_lds[e];
-      v.y = v.x;
-    }
-    return v;
-  };
-
-  float m_run = -INFINITY;  // running max of this lane's M-row (raw score units)
-  float l_run = 0.f;        // this lane's share of the exp-sum
-  f32x16 o[DT32];
-#pragma unroll
-  for (int n = 0; n < DT32; ++n)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[n][r] = 0.f;
-
-  // Key order inside a 32-key step.  The QK product's A operand takes key
-  // kperm(m) as its row m (bits 2 and 3 of m swapped); then the 8 scores a
-  // lane feeds into each PV k-step are 8 consecutive keys, and the V^T operand
-  // is one 16-byte LDS read per lane.  LDS already holds K in this row order.
-
-  // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d] for step st (raw scores).
-  auto read_k = [&](int st, u32x4 (&ka)[KS]) {
-    const int buf = st % kNBuf;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const int c = 2 * kk + half;  // stripe of dims 16kk + 8 half .. +7
-      ka[kk] = *reinterpret_cast<const u32x4*>(k_lds(buf) + IM::k_slot(col, c) * 8);
-    }
-  };
-  // V^T operand bases: k-step kk takes keys 16kk + 8 half .. +7; row tile n
-  // (dims 32n + col) sits kVRowTile slots further
-  const int v_base[2] = {IM::v_slot(col, 8 * half), IM::v_slot(col, 16 + 8 * half)};
-  // register r holds key k0 + 16 (r/8) + 8 half + 4 ((r/4)%2) + r%4 of
-  // M-row col.  Scores stay raw (the scale is positive, so maxima commute
-  // with it); the exponent is one fma: s * scale_log2 - m * scale_log2.
-  auto mask_score = [&](f32x16& sacc, int r, int st) {
-    const int key = st * kKeys + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
-    if (key >= my_lim) sacc[r] = -INFINITY;
-  };
-  // Given this lane's max bm of a step's scores: moves the running max to the
-  // row max if it grew by more than the headroom (rescaling this row's O and
-  // exp-sum), and returns the exponent offset of the step.
-  auto update_max = [&](float bm) {
-    bm = max_xor32(bm);
-    if (__ballot(bm > m_run + kLazyRescale * p.scale_inv_log2)) {
-      const bool grow = bm > m_run + kLazyRescale * p.scale_inv_log2;
-      const float m_new = fmaxf(m_run, bm);
-      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * p.scale_log2);
-      // rows whose max did not grow by more than the headroom keep their scale
-      const float a = grow ? alpha : 1.f;
-      if (grow) m_run = m_new;
-      l_run *= a;
-#pragma unroll
-      for (int n = 0; n < DT32; ++n) o[n] *= a;
-    }
-    return (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
-  };
-
-  // Pipeline.  Memory: three steps ahead.  Iteration st waits for step st+1
-  // (step st+2 may still be in flight), passes the barrier, and then issues
-  // the copies of step st+3 into the buffer of step st-1, which every
-  // wavefront finished reading before the barrier; hence four buffers.
-  // Compute, inside a wavefront: all operand reads of the iteration go out
-  // first; the QK MFMAs of step st+1 run beside the exponentials of step st,
-  // and the PV MFMAs of step st beside the exp-sum of step st and the row max
-  // of step st+1, which gives the next iteration its exponent offset.
-  if (nsteps > 0) {
-    stage_pids(0);
-    if (n_pid > kPidChunk) stage_pids(1);
-  }
-  __syncthreads();
-  auto wait_barrier = [&](int pending_steps) {  // all but the pending_steps youngest steps' copies landed
-    compiler_fence();
-    if (pending_steps >= 2)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NL));
-    else if (pending_steps == 1)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
-    else
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    __builtin_amdgcn_s_waitcnt(kLgkmZero);
-    __builtin_amdgcn_s_barrier();
-    compiler_fence();
-  };
-  f32x16 s_cur;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s_cur[r] = 0.f;
-  float mb = 0.f;
-  if (nsteps > 0) {
-    for (int j = 0; j < 3 && j < nsteps; ++j) {
-      const u32x2 pg = read_pids(j);
-      issue(j, __builtin_amdgcn_readfirstlane(pg.x), __builtin_amdgcn_readfirstlane(pg.y));
-    }
-    wait_barrier(min(nsteps - 1, 2));  // step 0 has landed
-    u32x4 ka[KS];
-    read_k(0, ka);
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) s_cur = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_cur);
-    float bm = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if (min_lim < kKeys) mask_score(s_cur, r, 0);
-      bm = fmaxf(bm, s_cur[r]);
-    }
-    mb = update_max(bm);
-  }
-  // Steps whose next step needs no mask (every row sees all its keys) run
-  // the unmasked body.  The last step is always in the masked part, whose
-  // mask also discards the scores of the stale buffer it reads as "next".
-  const int n_main = max(0, min(nsteps, min_lim / kKeys - 1));
-  auto step = [&](auto masked, int st) {
-    constexpr bool kMask = decltype(masked)::value;
-    wait_barrier(st + 2 < nsteps ? 1 : 0);  // step st+1 has landed
-    const int j = st + 3;
-    const u32x2 pgv = read_pids(j);  // used after the MFMAs (in bounds whether or not step j exists)
-    u32x4 ka[KS];
-    read_k(st + 1, ka);
-    float pe[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) pe[r] = fmaf(s_cur[r], p.scale_log2, mb);
-    // The rest is written in issue order, chunk by chunk, with scheduling
-    // fences between chunks (the compiler would otherwise keep two operand
-    // reads in flight, wait before every MFMA and bunch the vector work):
-    // each QK MFMA of step st+1 (K operands all read above) goes out with one
-    // V operand read of step st and a share of step st's exponentials and
-    // conversions; each PV MFMA of step st with a share of the exp-sum and of
-    // the row max of step st+1.
-    sched_fence();
-    // Raised wave priority through the MFMA chunks: the other wavefront on
-    // the SIMD is then more often in its vector/LDS phase while this one
-    // issues MFMAs (measured +1 % on config 4, -1 to -3 % time on config 5).
-    __builtin_amdgcn_s_setprio(1);
-    const int vbuf = st % kNBuf;
-    f32x16 s_next;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
-    u32x4 va[KS];  // PV operand m: k-step m / DT32, row tile m % DT32 (KS == 2 * DT32)
-    uint32_t pp[8];  // packed probabilities of the lane's scores 2q, 2q+1
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      s_next = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_next);
-      va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
-#pragma unroll
-      for (int r = kk * 16 / KS; r < (kk + 1) * 16 / KS; ++r) pe[r] = __builtin_amdgcn_exp2f(pe[r]);
-#pragma unroll
-      for (int q = kk * 8 / KS; q < (kk + 1) * 8 / KS; ++q) pp[q] = Dt<DT>::pack2(pe[2 * q], pe[2 * q + 1]);
-      sched_fence();
-    }
-    const u32x4 pb[2] = {u32x4{pp[0], pp[1], pp[2], pp[3]}, u32x4{pp[4], pp[5], pp[6], pp[7]}};
-    // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
-    // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
-    float bm = -INFINITY;
-#pragma unroll
-    for (int m = 0; m < KS; ++m) {
-      o[m % DT32] = Dt<DT>::mma32x32x16(va[m], pb[m / DT32], o[m % DT32]);
-#pragma unroll
-      for (int r = m * 16 / KS; r < (m + 1) * 16 / KS; ++r) {
-        l_run += pe[r];
-        if (kMask) mask_score(s_next, r, st + 1);
-        bm = fmaxf(bm, s_next[r]);
-      }
-      sched_fence();
-    }
-    __builtin_amdgcn_s_setprio(0);
-    mb = update_max(bm);
-    if (j < nsteps) {
-      // entering page-id chunk q (q >= 1): stage chunk q + 1 over chunk q - 1,
-      // whose last reader finished before this iteration's barrier; the next
-      // barriers publish it long before its first reader
-      const int e0 = j * kKeys / TPP;
-      if (e0 % kPidChunk == 0 && e0 > 0 && e0 + kPidChunk < n_pid) stage_pids(e0 / kPidChunk + 1);
-      issue(j, __builtin_amdgcn_readfirstlane(pgv.x), __builtin_amdgcn_readfirstlane(pgv.y));
-    }
-    s_cur = s_next;
-  };
-  int st = 0;
-  for (; st < n_main; ++st) step(std::false_type{}, st);
-  for (; st < nsteps; ++st) step(std::true_type{}, st);
-
-  // ---- normalise and write: lane holds O[M-row col][32n + 8(r/4) + 4 half + r%4]
-  float l = sum_xor32(l_run);
-  if (row_ok) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int64_t orow = static_cast<int64_t>(row0 + my_t) * p.num_q_heads + kvh * p.group + h0 + my_h;
-    uint16_t* op = p.out + orow * HD;
-#pragma unroll
-    for (int n = 0; n < DT32; ++n) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = 32 * n + 8 * q4 + 4 * half;
-        const u32x2 pk = {Dt<DT>::pack2(o[n][4 * q4 + 0] * inv, o[n][4 * q4 + 1] * inv),
-                          Dt<DT>::pack2(o[n][4 * q4 + 2] * inv, o[n][4 * q4 + 3] * inv)};
-        *reinterpret_cast<u32x2*>(op + d) = pk;
-      }
-    }
-  }
-}
-
-// Rows [0, R) of the query batch alternate runs of one sequence.  Is row r
-// alone in its run (a decode row, served by the decode kernels)?
-__device__ __forceinline__ bool single_row(const uint32_t* q2seq, int64_t r, int64_t n) {
-  const uint32_t sq = q2seq[r];
-  return (r == 0 || q2seq[r - 1] != sq) && (r + 1 == n || q2seq[r + 1] != sq);
-}
-
-// 1-D grid, XCD-aware: block b serves head group g = b % G (G = kv heads x
-// head chunks) and work unit b / G, so consecutive blocks -- which the
-// dispatcher spreads over the 8 XCDs -- take different kv heads, and each kv
-// head's K/V stay in few L2s.
-//  * prompt mode: unit = (sequence, tile), the last tile of a sequence first
-//    (it has the most keys);
-//  * window mode (fused op): unit = window of `tokens per tile` rows; every
-//    run of rows of one sequence inside the window that is not a lone decode
-//    row is computed as a tile.
+// One workgroup of tiles per block (the work mapping is in prefill_block).
 template <int DT, int HD, int TPP, bool KV8>
 __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kNBuf * StepGeo<HD>::kItems * 8];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kNBuf * StepGeo<HD>::kItems * 8];
-  __shared__ __attribute__((aligned(16))) uint16_t junk_lds[kWave * 8];  // target of the padding copies
-  __shared__ uint32_t pid_lds[2 * kPidChunk];
-  __shared__ int lim_lds[kMRows];
-  __shared__ int run_start[kMRows];
-  const int G = p.num_kv_heads * p.head_chunks;
-  const int g = static_cast<int>(blockIdx.x % static_cast<unsigned>(G));
-  const int unit = static_cast<int>(blockIdx.x / static_cast<unsigned>(G));
-  const int kvh = g / p.head_chunks;
-  const int h0 = (g % p.head_chunks) * 16;
-  const int qt = kMRows / p.hg_max;
-  if (p.prompt_len > 0) {
-    const int tps = (p.prompt_len + qt - 1) / qt;
-    const int s = unit / tps;
-    const int j = tps - 1 - (unit - s * tps);
-    const int row0 = s * p.prompt_len + j * qt;
-    prefill_tile<DT, HD, TPP, true, KV8>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, junk_lds,
-                                    pid_lds, lim_lds);
-    return;
-  }
-  const int w0 = unit * qt;
-  const int w1 = static_cast<int>(min(static_cast<int64_t>(w0 + qt), p.num_rows));
-  const int tid = threadIdx.x;
-  if (tid < w1 - w0) run_start[tid] = (tid == 0 || p.q2seq[w0 + tid] != p.q2seq[w0 + tid - 1]) ? 1 : 0;
-  __syncthreads();
-  int cur = w0;
-  while (cur < w1) {
-    int end = cur + 1;
-    while (end < w1 && !run_start[end - w0]) ++end;
-    end = __builtin_amdgcn_readfirstlane(end);
-    if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
-      prefill_tile<DT, HD, TPP, false, KV8>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
-                                       lim_lds);
-    cur = end;
-  }
+  __shared__ PrefillLds<HD> lds;
+  prefill_block<DT, HD, TPP, KV8>(p, blockIdx.x, lds);
 }
 
 template <int DT, int HD, int TPP, bool KV8>

@@ -25,7 +25,11 @@ int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partiti
   if (partition_size > 0) return resident + (max_blocks + partition_size / 16 - 1) / (partition_size / 16);
   return resident + 1;
 }
-hipError_t launch_decode(const DecodeParams&, int, int, int, bool, hipStream_t) { return hipErrorNoDevice; }
+hipError_t launch_decode(const DecodeParams&, int, int, int, hipStream_t) { return hipErrorNoDevice; }
+bool fused_shares_cu(int head_dim) { return head_dim <= 128; }
+hipError_t launch_fused(const DecodeParams&, const PrefillParams&, int, int, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
 int prefill_tokens_per_tile(int group) { return 128 / (group < 16 ? group : 16); }
 hipError_t launch_prefill(const PrefillParams&, int, int, int, hipStream_t) { return hipErrorNoDevice; }
 hipError_t launch_copy_pages(const PageCopyParams&, hipStream_t) { return hipErrorNoDevice; }

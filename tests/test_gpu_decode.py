@@ -127,7 +127,7 @@ def test_decode_partition_modes(hd, dtype, tpp, partition):
 @pytest.mark.parametrize("partition", [128, 512])
 def test_decode_partition_many_sequences(partition):
     """Fixed-chunk mode with more sequences than the in-kernel planner takes
-    (the separate plan kernel), zero lengths among them."""
+    (the separate plan kernel of plain decode), zero lengths among them."""
     rng = np.random.default_rng(17 + partition)
     lens = rng.integers(0, 700, size=1300).astype(np.int32)
     lens[rng.choice(1300, 50, replace=False)] = 0

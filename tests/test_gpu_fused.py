@@ -135,13 +135,23 @@ def test_fused_edge_rows():
 
 
 def test_fused_many_rows_planner_chunks():
-    """More than 1024 rows (the planner carries runs across its chunks and
-    the decode items take the separate plan kernel): 1100 decode rows plus a
-    1500-row prompt run split by the chunk boundary."""
+    """More than 1024 rows (the decode workers' row scan carries runs across
+    its passes of 4096 rows): 1100 decode rows plus a 1500-row prompt run."""
     rng = np.random.default_rng(63)
     dec = rng.integers(0, 80, size=1100)
     fc = make_fused_case(63, dec, [(200, 1500)], 8, 1, 64, 16, "f16", block=1500, garbage_tail=False)
     _check_fused(fc, "many rows")
+
+
+def test_fused_lone_rows_beyond_the_list():
+    """More lone (decode) rows with keys than the fused kernel's in-LDS list
+    holds (2048): the decode workers claim batches of 64 rows and compute each
+    lone row whole.  Rows without keys and a prompt run interleave."""
+    rng = np.random.default_rng(65)
+    dec = rng.integers(0, 400, size=2300)
+    fc = make_fused_case(65, dec, [(50, 300)], 8, 2, 64, 16, "bf16", block=100)
+    assert int(np.count_nonzero(dec)) > 2048
+    _check_fused(fc, "claiming mode")
 
 
 def test_fused_deterministic_and_empty():
