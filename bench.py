@@ -282,6 +282,17 @@ class FusedWorkload:
         self.queries = torch.randn((self.rows, hq, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
         self.decode_bytes = int(dec.astype(np.int64).sum()) * 2 * hkv * hd * 2 + 2 * 256 * hq * hd * 2
         self.prefill_flops = causal_flops(hq, hd, cached, new)
+        # the same rows split by kind (sequences 0..255 are the decode ones),
+        # for timing each half alone through the same operator
+        self.parts = {}
+        for name, sel in (("decode_rows", q2s < 256), ("prefill_rows", q2s >= 256)):
+            idx = torch.from_numpy(np.nonzero(sel)[0]).to(device)
+            self.parts[name] = (self.queries.index_select(0, idx).contiguous(), self.q2seq.index_select(0, idx),
+                                self.q_offset.index_select(0, idx))
+
+    def attend_part(self, name: str):
+        q, q2s, off = self.parts[name]
+        return pal.paged_attention(q, self.k_pool, self.v_pool, self.page_table, self.seq_lens, q2s, off)
 
     def attend(self):
         return pal.paged_attention(self.queries, self.k_pool, self.v_pool, self.page_table, self.seq_lens,
@@ -338,6 +349,12 @@ def cpu_baseline(w: DecodeWorkload, budget_s: float = 12.0) -> dict:
         cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:  # pragma: no cover
         cores = os.cpu_count() or 1
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), cpu_model)
+    except OSError:  # pragma: no cover
+        pass
     dt = "bf16"
     q = w.queries.view(torch.int16).cpu().numpy().view(np.uint16)
     kb = w.k_pool.view(torch.int16).cpu().numpy().view(np.uint16)
@@ -367,6 +384,8 @@ def cpu_baseline(w: DecodeWorkload, budget_s: float = 12.0) -> dict:
         "unit": "GB/s",
         "tokens_per_s": round(ns / el, 2),
         "cores": int(cores),
+        "cpu_model": cpu_model,
+        "affinity_cpus": len(os.sched_getaffinity(0)),
         "kind": "port",
         "sample": f"numpy oracle (bf16->fp32 decode of the sample's pages, gather, fp32 softmax attention) on "
                   f"{ns} of the 64 config-2 sequences ({int(lens.sum())} context tokens), {reps} reps in "
@@ -576,12 +595,16 @@ def run_extra(configs: set[str], dev, args) -> dict:
     if "c5" in configs:
         w = FusedWorkload(dev)
         ms, _ = time_op(w.attend, steps, warm, stream)
+        dec_ms, _ = time_op(lambda: w.attend_part("decode_rows"), steps, warm, stream)
+        pre_ms, _ = time_op(lambda: w.attend_part("prefill_rows"), steps, warm, stream)
         t_roof_ms = (w.decode_bytes / (HBM_PEAK_GBS * 1e9) + w.prefill_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12)) * 1e3
         out["fused"] = {
             "workload": "config 5: 256 decode rows ctx U[256,8192] + 4 x 1024 prefill rows on U[0,4096] cached, "
                         "64/8 heads, HD 128, fp16, shuffled row blocks, one paged_attention call",
             "rows": w.rows, "decode_bytes": w.decode_bytes, "prefill_flops": w.prefill_flops,
             "ms": round(ms, 4), "roofline_ms": round(t_roof_ms, 4), "frac_of_roofline": round(t_roof_ms / ms, 4),
+            "decode_rows_alone_ms": round(dec_ms, 4), "prefill_rows_alone_ms": round(pre_ms, 4),
+            "ms_over_sum_of_halves": round(ms / (dec_ms + pre_ms), 4),
         }
         del w
         torch.cuda.empty_cache()
