@@ -136,6 +136,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
                                              uint16_t* k_lds_base, uint16_t* v_lds_base, uint16_t* junk_lds,
                                              uint32_t* pid_lds, int* lim_lds) {
   static_assert(HD % 32 == 0, "prefill needs head_dim % 32 == 0");
+  static_assert(2 * StepGeo<HD>::kLoads <= HD / 16, "a step's copies fit in its PV chunks");
   constexpr int KS = HD / 16;  // QK k-steps of 16
   constexpr int DT32 = HD / 32;  // O^T row tiles of 32 dims
   constexpr int NI = StepGeo<HD>::kItems;
@@ -252,36 +253,42 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   __builtin_assume(w >= 0 && w < kPfWaves);
   // page ids >= 2^32 - 1 cannot occur with fewer pages; such an id takes the slow path
   const uint32_t np32 = p.num_pages > 0xFFFFFFFFll ? 0xFFFFFFFFu : static_cast<uint32_t>(p.num_pages);
+  // Copy q of a fast step into buffer buf: the K items (q < NL) or the V
+  // items (q >= NL) of this thread's load q % NL, off0 / off1 the (page,
+  // kv head) blocks of the step's two pages.
+  auto copy_one = [&](int q, int buf, int64_t off0, int64_t off1) {
+    const int jj = q % NL;
+    const int i = tid + jj * kPfThreads;
+    const int ib = w * kWave + jj * kPfThreads;  // first item of this wavefront's load
+    const bool ok = kAllItems || ib < NI;
+    if (q < NL) {
+      const uint16_t* page = p.k_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
+      const uint32_t src = 2u * static_cast<uint32_t>(ok ? IM::k_offset(i) : 0);
+      copy_to_lds16(page, src, lds_addr(ok ? k_lds(buf) + ib * 8 : junk_lds));
+    } else {
+      const uint16_t* page = p.v_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
+      int d = 0, key = 0;
+      if (ok) IM::v_item(i, d, key);
+      const uint32_t src = 2u * static_cast<uint32_t>(d * TPP + key % TPP);
+      copy_to_lds16(page, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
+    }
+  };
+  // step j takes the fast path (fp8 pools take the register path: the
+  // copies cannot dequantize)
+  auto is_fast = [&](int j, uint32_t pg0, uint32_t pg1) {
+    const int k0 = j * kKeys;
+    return !KV8 && k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
+  };
   auto issue = [&](int j, uint32_t pg0, uint32_t pg1) {
     const int buf = j % kNBuf;
     const int k0 = j * kKeys;
     if (TPP != 16) pg1 = pg0;
-    // fp8 pools take the register path: the copies cannot dequantize
-    const bool fast = !KV8 && k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 &&
-                      (!prompt_mode || k0 + kKeys <= hist);
+    const bool fast = is_fast(j, pg0, pg1);
     if (fast) {
       const int64_t off0 = static_cast<int64_t>(pg0) * page_stride + kv_head_off;
       const int64_t off1 = static_cast<int64_t>(pg1) * page_stride + kv_head_off;
 #pragma unroll
-      for (int jj = 0; jj < NL; ++jj) {
-        const int i = tid + jj * kPfThreads;
-        const int ib = w * kWave + jj * kPfThreads;  // first item of this wavefront's load
-        const bool ok = kAllItems || ib < NI;
-        const uint16_t* page = p.k_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
-        const uint32_t src = 2u * static_cast<uint32_t>(ok ? IM::k_offset(i) : 0);
-        copy_to_lds16(page, src, lds_addr(ok ? k_lds(buf) + ib * 8 : junk_lds));
-      }
-#pragma unroll
-      for (int jj = 0; jj < NL; ++jj) {
-        const int i = tid + jj * kPfThreads;
-        const int ib = w * kWave + jj * kPfThreads;
-        const bool ok = kAllItems || ib < NI;
-        const uint16_t* page = p.v_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
-        int d = 0, key = 0;
-        if (ok) IM::v_item(i, d, key);
-        const uint32_t src = 2u * static_cast<uint32_t>(d * TPP + key % TPP);
-        copy_to_lds16(page, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
-      }
+      for (int q = 0; q < 2 * NL; ++q) copy_one(q, buf, off0, off1);
       return;
     }
 #pragma unroll
@@ -525,8 +532,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
     // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
     float bm = -INFINITY;
+    // A fast step j issues its copies one per PV chunk (the first 2 NL
+    // chunks), so the wavefront's MFMAs run while an issue waits for the
+    // memory pipeline (measured 3 % on config 4 against issuing them all
+    // after the chunks); other steps take the synchronous path below.
+    const uint32_t jp0 = __builtin_amdgcn_readfirstlane(pgv.x);
+    const uint32_t jp1 = TPP == 16 ? __builtin_amdgcn_readfirstlane(pgv.y) : jp0;
+    const bool jfast = j < nsteps && is_fast(j, jp0, jp1);
+    const int64_t joff0 = static_cast<int64_t>(jp0) * page_stride + kv_head_off;
+    const int64_t joff1 = static_cast<int64_t>(jp1) * page_stride + kv_head_off;
 #pragma unroll
     for (int m = 0; m < KS; ++m) {
+      if (jfast && m < 2 * NL) copy_one(m, j % kNBuf, joff0, joff1);
       o[m % DT32] = Dt<DT>::mma32x32x16(va[m], pb[m / DT32], o[m % DT32]);
       // the exp-sum adds the probabilities as rounded for the PV product
 #pragma unroll
@@ -546,7 +563,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       // barriers publish it long before its first reader
       const int e0 = j * kKeys / TPP;
       if (e0 % kPidChunk == 0 && e0 > 0 && e0 + kPidChunk < n_pid) stage_pids(e0 / kPidChunk + 1);
-      issue(j, __builtin_amdgcn_readfirstlane(pgv.x), __builtin_amdgcn_readfirstlane(pgv.y));
+      if (!jfast) issue(j, jp0, jp1);
     }
     s_cur = s_next;
   };
