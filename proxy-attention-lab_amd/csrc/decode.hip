@@ -852,7 +852,7 @@ __device__ __forceinline__ void fused_claim_rows(const DecodeParams& p, FusedDec
     const int64_t batch = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(k)) * kWave;
     if (batch >= n_rows) break;
     const int64_t r = batch + lane;
-    int64_t len = 0;
+    int32_t len = 0;
     bool keep = false;
     if (r < n_rows) {
       const uint32_t prev = r > 0 ? p.q2seq[r - 1] : 0xFFFFFFFFu;
@@ -896,15 +896,15 @@ __device__ __forceinline__ void fused_decode_body(const DecodeParams& p, FusedDe
   const int64_t segs = static_cast<int64_t>(p.num_kv_heads) * p.head_chunks;
   const int64_t max_tokens = p.page_table_width * TPP;
   // a row's sequence, keys and whether it is a lone row with keys
-  auto lone_row = [&](int64_t r, uint32_t prev, uint32_t sq, uint32_t next, int64_t& len) {
+  auto lone_row = [&](int64_t r, uint32_t prev, uint32_t sq, uint32_t next, int32_t& len) {
     len = 0;
     if ((r > 0 && prev == sq) || (r + 1 < n_rows && next == sq)) return false;  // a prefill row
     if (sq < p.num_pt_rows) {
       const int64_t l = p.seq_lens[sq];
       const int64_t off = p.q_offset[r];
-      len = off < l ? off : l;
-      PAL_DEBUG_FLAG(len > max_tokens, kDebugLength);
-      len = len < 0 ? 0 : (len > max_tokens ? max_tokens : len);
+      const int64_t k = off < l ? off : l;
+      PAL_DEBUG_FLAG(k > max_tokens, kDebugLength);
+      len = static_cast<int32_t>(k < 0 ? 0 : (k > max_tokens ? max_tokens : k));
     }
     if (len == 0 && blockIdx.x == 0) zero_item_output<HD>(p, r);  // no key: zeros, once
     return len > 0;
@@ -919,7 +919,7 @@ __device__ __forceinline__ void fused_decode_body(const DecodeParams& p, FusedDe
       const int64_t r = r0 - 1 + k;
       sq[k] = (r >= 0 && r < n_rows) ? p.q2seq[r] : 0xFFFFFFFFu;
     }
-    int64_t lens[kFusedScanPer];
+    int32_t lens[kFusedScanPer];  // keys (< 2^31: a page-table row holds fewer tokens)
     int64_t cnt = 0, blk = 0;
 #pragma unroll
     for (int k = 0; k < kFusedScanPer; ++k) {

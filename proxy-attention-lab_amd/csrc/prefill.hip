@@ -22,8 +22,16 @@ namespace pal {
 namespace {
 
 // One workgroup of tiles per block (the work mapping is in prefill_block).
+// Head dims up to 128 are held to half of the register file (two wavefronts
+// per SIMD); head dim 256 needs more than that and runs one per SIMD.
 template <int DT, int HD, int TPP, bool KV8>
-__global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_tile_kernel(const PrefillParams p) {
+  __shared__ PrefillLds<HD> lds;
+  prefill_block<DT, HD, TPP, KV8>(p, blockIdx.x, lds);
+}
+template <int DT, int HD, int TPP, bool KV8>
+__global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel_wide(const PrefillParams p) {
   __shared__ PrefillLds<HD> lds;
   prefill_block<DT, HD, TPP, KV8>(p, blockIdx.x, lds);
 }
@@ -31,8 +39,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel(const PrefillP
 template <int DT, int HD, int TPP, bool KV8>
 hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
   const int64_t blocks = static_cast<int64_t>(p.num_units) * p.num_kv_heads * p.head_chunks;
-  hipLaunchKernelGGL((prefill_tile_kernel<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(blocks)), dim3(kPfThreads),
-                     0, stream, p);
+  if constexpr (HD <= 128)
+    hipLaunchKernelGGL((prefill_tile_kernel<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kPfThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prefill_tile_kernel_wide<DT, HD, TPP, KV8>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kPfThreads), 0, stream, p);
   return hipGetLastError();
 }
 
