@@ -910,6 +910,40 @@ __device__ __forceinline__ void fused_decode_body(const DecodeParams& p, FusedDe
     return len > 0;
   };
 
+  // Quick pass: is any row alone in its run?  Lane t of a pass reads rows
+  // 4t .. 4t+3 as one 16-byte load (when the map is 16-byte aligned) and
+  // their two neighbours; a batch with none (a prefill-only batch) ends here.
+  {
+    bool any = false;
+    const bool vec = (reinterpret_cast<uintptr_t>(p.q2seq) & 15u) == 0;
+    for (int64_t base = 0; base < n_rows; base += 4 * kGroupThreads) {
+      const int64_t r0 = base + 4 * static_cast<int64_t>(tid);
+      if (r0 >= n_rows) continue;
+      uint32_t q[6];
+      q[0] = r0 > 0 ? p.q2seq[r0 - 1] : 0xFFFFFFFFu;
+      if (vec && r0 + 4 <= n_rows) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p.q2seq + r0);
+        q[1] = v.x;
+        q[2] = v.y;
+        q[3] = v.z;
+        q[4] = v.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[1 + k] = r0 + k < n_rows ? p.q2seq[r0 + k] : 0xFFFFFFFFu;
+      }
+      q[5] = r0 + 4 < n_rows ? p.q2seq[r0 + 4] : 0xFFFFFFFFu;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t r = r0 + k;
+        if (r < n_rows && (r == 0 || q[k] != q[k + 1]) && (r + 1 == n_rows || q[k + 2] != q[k + 1])) any = true;
+      }
+    }
+    if (!__syncthreads_or(any)) {
+      if (blockIdx.x == 0 && tid == 0) p.hdr[0] = 0;  // nothing to merge
+      return;
+    }
+  }
+
   int64_t n_lone = 0, n_blocks = 0;  // running totals (uniform)
   for (int64_t base = 0; base < n_rows; base += static_cast<int64_t>(kGroupThreads) * kFusedScanPer) {
     const int64_t r0 = base + static_cast<int64_t>(tid) * kFusedScanPer;

@@ -297,8 +297,8 @@ def test_prefill_fp8_history(dtype, hd, tpp):
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("hd,tpp", [(128, 16), (64, 32), (256, 16)])
 def test_fused_fp8_pages(dtype, hd, tpp):
-    """A mixed batch over fp8 pages: decode rows (the fused op's shared-CU
-    decode, or the stream kernel at head_dim 256) and prefill runs."""
+    """A mixed batch over fp8 pages: decode rows (the fused kernel's decode
+    workers, or the stream kernel at head_dim 256) and prefill runs."""
     from pal_cases import make_fused_case
 
     rng = np.random.default_rng(hd * 3 + tpp)
@@ -315,3 +315,24 @@ def test_fused_fp8_pages(dtype, hd, tpp):
     ref = orc.paged_attention(fc.queries, kc, vc, c.page_table, c.seq_lens, fc.q2seq, fc.q_offset, dtype,
                               kv_scales=(ks, vs))
     assert_close(host_f32(out), ref, dtype, f"fp8 fused {dtype} hd{hd} tpp{tpp}")
+
+
+def test_fused_fp8_claiming_mode():
+    """More than 2048 lone rows with keys over fp8 pages at head_dim 128: the
+    fused kernel's decode workers claim row batches and compute rows whole."""
+    from pal_cases import make_fused_case
+
+    rng = np.random.default_rng(71)
+    dec = rng.integers(1, 200, size=2100)
+    fc = make_fused_case(71, dec, [(20, 150)], 16, 4, 128, 16, "f16", block=50)
+    c = fc.case
+    kc, vc, ks, vs = fp8_case(c, rng)
+    announce("fused fp8 pages, claiming mode (2100 lone rows)")
+    out = pal.paged_attention(dev_bits(fc.queries, "f16"), dev_codes(kc), dev_codes(vc),
+                              dev_index(c.page_table, torch.uint32), dev_index(c.seq_lens),
+                              dev_index(fc.q2seq, torch.uint32), dev_index(fc.q_offset),
+                              k_scales=torch.from_numpy(ks).to(DEV), v_scales=torch.from_numpy(vs).to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.paged_attention(fc.queries, kc, vc, c.page_table, c.seq_lens, fc.q2seq, fc.q_offset, "f16",
+                              kv_scales=(ks, vs))
+    assert_close(host_f32(out), ref, "f16", "fp8 fused claiming mode")
