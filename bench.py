@@ -299,6 +299,33 @@ class FusedWorkload:
                                    self.q2seq, self.q_offset)
 
 
+class PromptWorkload:
+    """The reference prefill signature (paged_attention_prefill): 16 sequences
+    x 1024 prompt rows on U[0,2048] cached history, 32/8 heads, HD 128, bf16;
+    history keys from pages, prompt keys from the dense prompt K/V rows."""
+
+    def __init__(self, device, seed: int = 11, num_seqs=16, prompt=1024, hq=32, hkv=8, hd=128, dtype=torch.bfloat16):
+        rng = np.random.default_rng(6000 + seed)
+        self.hist = rng.integers(0, 2049, size=num_seqs).astype(np.int32)
+        g = torch.Generator(device=device)
+        g.manual_seed(7000 + seed)
+        self.k_pool, self.v_pool, pt = paged_pool(rng, g, np.maximum(self.hist, 1), hkv, hd, 16, dtype, device)
+        self.page_table = torch.from_numpy(pt).to(device)
+        self.context_lens = torch.from_numpy(self.hist).to(device)
+        n = num_seqs * prompt
+        self.prompt, self.hq, self.hd = prompt, hq, hd
+        self.q = torch.randn((n, hq, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+        self.k = torch.randn((n, hkv, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+        self.v = torch.randn((n, hkv, hd), generator=g, device=device, dtype=torch.float32).to(dtype)
+
+    def attend(self):
+        return pal.paged_attention_prefill(self.q, self.k, self.v, self.k_pool, self.v_pool, self.page_table,
+                                           self.context_lens)
+
+    def flops(self) -> float:
+        return causal_flops(self.hq, self.hd, self.hist, np.full(len(self.hist), self.prompt, np.int32))
+
+
 class RopeFill:
     """The fused RoPE + cast + scatter feeding a fill step: fp32 projection
     rows (K, V and the queries) of the workload's new tokens, NeoX rotation
@@ -591,6 +618,17 @@ def run_extra(configs: set[str], dev, args) -> dict:
         out["prefill"]["rope_fill"] = rope.report(rope_ms)
         del rope
         del w
+        torch.cuda.empty_cache()
+        pw = PromptWorkload(dev)
+        p_ms, _ = time_op(pw.attend, steps, warm, stream)
+        p_tf = pw.flops() / (p_ms * 1e-3) / 1e12
+        out["prefill"]["reference_signature"] = {
+            "workload": "paged_attention_prefill: 16 seqs x 1024 prompt rows on U[0,2048] cached history, "
+                        "32/8 heads, HD 128, bf16 (history keys from pages, prompt keys from the prompt rows)",
+            "causal_flops": pw.flops(), "ms": round(p_ms, 4), "TFLOP/s": round(p_tf, 1),
+            "frac_of_mfma_bf16_peak": round(p_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+        }
+        del pw
         torch.cuda.empty_cache()
     if "c5" in configs:
         w = FusedWorkload(dev)

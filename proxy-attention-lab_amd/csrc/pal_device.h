@@ -186,6 +186,17 @@ __device__ __forceinline__ void copy_to_lds16(const void* base, uint32_t off, ui
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16).  In each group of 16 lanes,
+// lane 4r + c points at 4 consecutive 16-bit elements, columns 4c .. 4c+3 of
+// row r of a 4 x 16 block; lane j receives column j, rows 0..3 (element i in
+// bits 16i .. 16i+15).  The address must be 8-byte aligned.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4* lds_s16x4;
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
 // Scheduling fence: the compiler's instruction scheduler moves nothing
 // across this point (data dependences are unaffected; waits are inserted
 // as usual).

@@ -16,8 +16,11 @@
 //  * Per 32-key step the K and V tiles reach LDS by direct-to-LDS copies
 //    (global_load_lds_dwordx4, no registers), issued two steps ahead into four
 //    LDS buffers, with counted waits and one barrier per step.  Page ids come
-//    from an LDS copy of the tile's page-table slice.  Steps at the tile end
-//    or with dense prompt keys take a synchronous register path.
+//    from an LDS copy of the tile's page-table slice.  Steps of dense prompt
+//    keys are copied the same way from the prompt rows (V rows untransposed,
+//    read back with transposing LDS reads).  Steps at the tile end, across
+//    the history / prompt boundary or in fp8 pools take a synchronous
+//    register path.
 //  * Each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
 //    from LDS, B = Q^T held in registers) and O^T += V^T * P^T with the same
 //    instruction.  In the transposed products a lane owns one M-row, so the
@@ -245,7 +248,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // no registers, nothing to wait for here.  Every wavefront issues exactly
   // 2*NL copies (items past the step go to a junk slot), so the wait counts
   // are the same on every wavefront.
-  // Slow step (tile end, invalid pages, dense prompt keys): register loads,
+  // Slow step (tile end, invalid pages, history / prompt boundary, fp8): register loads,
   // masked, then LDS stores -- synchronous, so it also drains the copies in
   // flight, which keeps the counted waits safe.
   // pg0 / pg1: the pages of the step's first and (TPP 16) second 16 keys.
@@ -279,9 +282,51 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     const int k0 = j * kKeys;
     return !KV8 && k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
   };
+  // Prompt mode: a step whose 32 keys are all prompt keys below the tile's
+  // largest limit copies them from the dense prompt rows (16-bit in every
+  // pool dtype): K into its operand layout, V rows untransposed (V items of
+  // the row layout are 16 contiguous bytes of one key; the PV operand reads
+  // of such a step transpose).
+  auto is_dense = [&](int j) {
+    const int k0 = j * kKeys;
+    return PROMPT && k0 >= hist && k0 + kKeys <= max_lim;
+  };
+  // Untransposed V rows, read back with transposing reads: each 16-lane
+  // group reads 32 bytes of each of 4 consecutive keys, the other group of
+  // its half-wavefront the next 32 bytes.  16-byte chunk c of key k is stored
+  // at chunk c ^ vd_swz(k), which puts a 16-lane group on distinct banks in a
+  // 32-bank pass and a half-wavefront on distinct banks in a 64-bank pass
+  // (HD 96 rows are not swizzled).
+  auto vd_swz = [](int key) {
+    const int r = key & 3;
+    return HD % 128 == 0 ? 4 * r + 2 * (r >> 1) : (HD == 64 ? 2 * r : (HD == 32 ? 2 * (r >> 1) : 0));
+  };
+  auto copy_dense = [&](int q, int buf, int j) {
+    const int jj = q % NL;
+    const int i = tid + jj * kPfThreads;
+    const int ib = w * kWave + jj * kPfThreads;
+    const bool ok = kAllItems || ib < NI;
+    const int64_t row0 = (dense_row0 + j * kKeys) * dense_stride + kvh * HD;  // key 0 of the step, this kv head
+    if (q < NL) {  // K in its operand layout, as from pages
+      int c = 0, key = 0;
+      if (ok) IM::k_item(i, c, key);
+      const uint32_t src = 2u * static_cast<uint32_t>(key * dense_stride + c * 8);
+      copy_to_lds16(p.k_dense + row0, src, lds_addr(ok ? k_lds(buf) + ib * 8 : junk_lds));
+    } else {
+      // raw rows: slot i = (key, 8-dim chunk c ^ vd_swz(key))
+      const int key = ok ? i / (HD / 8) : 0, c = ok ? (i % (HD / 8)) ^ vd_swz(key) : 0;
+      const uint32_t src = 2u * static_cast<uint32_t>(key * dense_stride + c * 8);
+      copy_to_lds16(p.v_dense + row0, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
+    }
+  };
   auto issue = [&](int j, uint32_t pg0, uint32_t pg1) {
     const int buf = j % kNBuf;
     const int k0 = j * kKeys;
+    if (is_dense(j)) {
+#pragma unroll
+      for (int q = 0; q < 2 * NL; ++q) copy_dense(q, buf, j);
+      return;
+    }
     if (TPP != 16) pg1 = pg0;
     const bool fast = is_fast(j, pg0, pg1);
     if (fast) {
@@ -513,6 +558,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // issues MFMAs (measured +1 % on config 4, -1 to -3 % time on config 5).
     __builtin_amdgcn_s_setprio(1);
     const int vbuf = st % kNBuf;
+    const bool vdense = is_dense(st);  // step st's V rows were copied untransposed
     f32x16 s_next;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
@@ -521,7 +567,21 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       s_next = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_next);
-      va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
+      if (vdense) {
+        // raw rows: V[key][d] in chunk (d / 8) ^ vd_swz(key) of row key.  Lane
+        // 4r + c of a 16-lane group points at keys kg + 4t + r, dims d0 + 4c ..
+        // +3 (d0 = 32 (kk % DT32) + (col & 16)); the transposing read hands
+        // lane j dim d0 + j = col + 32 (kk % DT32) of those 4 keys.
+        const int l16 = lane & 15;
+        const int key = 16 * (kk / DT32) + 8 * half + (l16 >> 2);
+        const int d = 32 * (kk % DT32) + (col & 16) + 4 * (l16 & 3);
+        const uint16_t* vr = v_lds(vbuf) + key * HD + (((d >> 3) ^ vd_swz(key)) << 3) + (d & 7);
+        const u32x2 lo = lds_read_tr16(vr);           // keys kg .. kg+3
+        const u32x2 hi = lds_read_tr16(vr + 4 * HD);  // keys kg+4 .. kg+7 (vd_swz(key + 4) = vd_swz(key))
+        va[kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
+      }
 #pragma unroll
       for (int r = kk * 16 / KS; r < (kk + 1) * 16 / KS; ++r) pe[r] = __builtin_amdgcn_exp2f(pe[r]);
 #pragma unroll
@@ -538,12 +598,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // after the chunks); other steps take the synchronous path below.
     const uint32_t jp0 = __builtin_amdgcn_readfirstlane(pgv.x);
     const uint32_t jp1 = TPP == 16 ? __builtin_amdgcn_readfirstlane(pgv.y) : jp0;
-    const bool jfast = j < nsteps && is_fast(j, jp0, jp1);
+    const bool jdense = j < nsteps && is_dense(j);
+    const bool jfast = j < nsteps && (jdense || is_fast(j, jp0, jp1));
     const int64_t joff0 = static_cast<int64_t>(jp0) * page_stride + kv_head_off;
     const int64_t joff1 = static_cast<int64_t>(jp1) * page_stride + kv_head_off;
 #pragma unroll
     for (int m = 0; m < KS; ++m) {
-      if (jfast && m < 2 * NL) copy_one(m, j % kNBuf, joff0, joff1);
+      if (jfast && m < 2 * NL) {
+        if (jdense)
+          copy_dense(m, j % kNBuf, j);
+        else
+          copy_one(m, j % kNBuf, joff0, joff1);
+      }
       o[m % DT32] = Dt<DT>::mma32x32x16(va[m], pb[m / DT32], o[m % DT32]);
       // the exp-sum adds the probabilities as rounded for the PV product
 #pragma unroll

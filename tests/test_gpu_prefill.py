@@ -125,3 +125,13 @@ def test_prefill_long_history_page_id_chunks(tpp, hist):
     or four chunks, so the kernel stages later chunks over earlier ones while
     the key loop runs."""
     _check(31 + tpp, hist, 48, 32, 8, 128, tpp, "bf16", f"long history tpp{tpp}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hd", [32, 64, 96, 128, 256])
+def test_prefill_dense_prompt_steps(hd, dtype):
+    """Prompts long enough that most 32-key steps lie wholly in the prompt:
+    those steps copy K/V straight from the prompt rows (V untransposed, read
+    back with transposing LDS reads), after paged steps of histories that end
+    on and off a step boundary."""
+    _check(70 + hd, [0, 64, 96, 31, 33], 160, 16, 4, hd, 16, dtype, f"dense prompt steps hd{hd}")
