@@ -278,9 +278,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   };
   // step j takes the fast path (fp8 pools take the register path: the
   // copies cannot dequantize)
+  // (the tile's last step may end past max_lim: its copies then read keys
+  // no row sees, from valid pages, and fix_tail clears their V entries)
   auto is_fast = [&](int j, uint32_t pg0, uint32_t pg1) {
     const int k0 = j * kKeys;
-    return !KV8 && k0 + kKeys <= max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
+    return !KV8 && k0 < max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
   };
   // Prompt mode: a step whose 32 keys are all prompt keys below the tile's
   // largest limit copies them from the dense prompt rows (16-bit in every
@@ -289,7 +291,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // of such a step transpose).
   auto is_dense = [&](int j) {
     const int k0 = j * kKeys;
-    return PROMPT && k0 >= hist && k0 + kKeys <= max_lim;
+    return PROMPT && k0 >= hist && k0 < max_lim;
   };
   // Untransposed V rows, read back with transposing reads: each 16-lane
   // group reads 32 bytes of each of 4 consecutive keys, the other group of
@@ -307,15 +309,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     const int ib = w * kWave + jj * kPfThreads;
     const bool ok = kAllItems || ib < NI;
     const int64_t row0 = (dense_row0 + j * kKeys) * dense_stride + kvh * HD;  // key 0 of the step, this kv head
+    const int last = max_lim - 1 - j * kKeys;  // keys past it (tile's last step) read this key's row instead
     if (q < NL) {  // K in its operand layout, as from pages
       int c = 0, key = 0;
       if (ok) IM::k_item(i, c, key);
-      const uint32_t src = 2u * static_cast<uint32_t>(key * dense_stride + c * 8);
+      const uint32_t src = 2u * static_cast<uint32_t>(min(key, last) * dense_stride + c * 8);
       copy_to_lds16(p.k_dense + row0, src, lds_addr(ok ? k_lds(buf) + ib * 8 : junk_lds));
     } else {
       // raw rows: slot i = (key, 8-dim chunk c ^ vd_swz(key))
       const int key = ok ? i / (HD / 8) : 0, c = ok ? (i % (HD / 8)) ^ vd_swz(key) : 0;
-      const uint32_t src = 2u * static_cast<uint32_t>(key * dense_stride + c * 8);
+      const uint32_t src = 2u * static_cast<uint32_t>(min(key, last) * dense_stride + c * 8);
       copy_to_lds16(p.v_dense + row0, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
     }
   };
@@ -420,6 +423,39 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       }
     }
   };
+  // The tile's last step j, when it ends past max_lim and was copied: the
+  // keys no row sees hold whatever the pages (or, in prompt mode, the row of
+  // the last key) held, and a masked probability of 0 times a NaN there
+  // would still be NaN, so their V entries are cleared.  Each thread clears
+  // its own items, after the barrier that saw the copies land and before the
+  // barrier preceding the step's V reads (a slow step's entries are zero
+  // already).
+  auto fix_tail = [&](int j) {
+    const int valid0 = max_lim - j * kKeys;  // valid keys of the step, 1 .. 31
+    uint16_t* vb = v_lds(j % kNBuf);
+    const bool dense = is_dense(j);
+#pragma unroll
+    for (int jj = 0; jj < NL; ++jj) {
+      const int i = tid + jj * kPfThreads;
+      if (i >= NI) continue;
+      u32x4* slot = reinterpret_cast<u32x4*>(vb + i * 8);
+      if (dense) {  // raw rows: slot i holds 8 dims of key i / (HD / 8)
+        if (i / (HD / 8) >= valid0) *slot = u32x4{0u, 0u, 0u, 0u};
+      } else {  // operand layout: 8 keys key .. key+7 of row d
+        int d, key;
+        IM::v_item(i, d, key);
+        const int valid = valid0 - key;
+        if (valid < 8) {
+          u32x4 val = *slot;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            val[e] &= (2 * e < valid ? 0x0000FFFFu : 0u) | (2 * e + 1 < valid ? 0xFFFF0000u : 0u);
+          *slot = val;
+        }
+      }
+    }
+  };
+  const bool tail_partial = max_lim % kKeys != 0;  // the last step ends past max_lim
   // the page ids of step j (an LDS broadcast read; TPP 32: one page)
   auto read_pids = [&](int j) {
     const int e = (j * kKeys / TPP) % (2 * kPidChunk);
@@ -519,6 +555,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       issue(j, __builtin_amdgcn_readfirstlane(pg.x), __builtin_amdgcn_readfirstlane(pg.y));
     }
     wait_barrier(min(nsteps - 1, 2));  // step 0 has landed
+    if (nsteps == 1 && tail_partial) fix_tail(0);
     u32x4 ka[KS];
     read_k(0, ka);
 #pragma unroll
@@ -542,6 +579,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     const u32x2 pgv = read_pids(j);  // used after the MFMAs (in bounds whether or not step j exists)
     u32x4 ka[KS];
     read_k(st + 1, ka);
+    if (kMask && st + 2 == nsteps && tail_partial) fix_tail(st + 1);
     float pe[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) pe[r] = fmaf(s_cur[r], p.scale_log2, mb);
