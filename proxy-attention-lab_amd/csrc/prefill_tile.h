@@ -720,9 +720,10 @@ struct PrefillLds {
 // heads, and each kv head's K/V stay in few L2s.
 //  * prompt mode: unit = (sequence, tile), the last tile of a sequence first
 //    (it has the most keys);
-//  * window mode (fused op): unit = window of `tokens per tile` rows; every
-//    run of rows of one sequence inside the window that is not a lone decode
-//    row is computed as a tile.
+//  * window mode (fused op): unit = window of `tokens per tile` rows, the
+//    last window first (rows of a sequence usually come in position order,
+//    so its later windows see more keys); every run of rows of one sequence
+//    inside the window that is not a lone decode row is computed as a tile.
 template <int DT, int HD, int TPP, bool KV8>
 __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned block, PrefillLds<HD>& L) {
   uint16_t* k_lds = L.k;
@@ -746,7 +747,9 @@ __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned b
                                     pid_lds, lim_lds);
     return;
   }
-  const int w0 = unit * qt;
+  // windows in reverse row order: a sequence's later rows see more keys, so
+  // its longest tiles start first and the grid ends on short ones
+  const int w0 = (p.num_units - 1 - unit) * qt;
   const int w1 = static_cast<int>(min(static_cast<int64_t>(w0 + qt), p.num_rows));
   const int tid = threadIdx.x;
   if (tid < w1 - w0) run_start[tid] = (tid == 0 || p.q2seq[w0 + tid] != p.q2seq[w0 + tid - 1]) ? 1 : 0;

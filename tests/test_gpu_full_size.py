@@ -144,3 +144,29 @@ def test_config3_full_size_decode(partition):
     ref = orc.paged_attention_decode(q_bits, kb, vb, spt, w.lens_np[seqs], "bf16")
     assert_close(out_h[seqs], ref, "bf16", f"config 3 partition {partition} seqs {seqs} "
                                           f"(ctx {[int(w.lens_np[s]) for s in seqs]})")
+
+
+def test_reference_signature_full_size():
+    """The reference prefill signature as bench.py builds it (16 x 1024
+    prompt rows on U[0,2048] cached history, 32/8 heads, HD 128, bf16):
+    finite everywhere; the sequences with the longest and the shortest
+    history re-checked on the oracle."""
+    announce("reference-signature prefill full size: build")
+    w = bench.PromptWorkload(DEV)
+    announce("reference-signature prefill full size: run")
+    out = w.attend()
+    torch.cuda.synchronize()
+    out_h = host_f32(out)
+    P, hq, hd = w.prompt, w.hq, w.hd
+    S = len(w.hist)
+    assert out_h.shape == (S * P * hq, hd)
+    assert np.isfinite(out_h).all()
+    seqs = sorted({int(np.argmax(w.hist)), int(np.argmin(w.hist))})
+    pt = w.page_table.cpu().numpy().astype(np.uint32)
+    kb, vb, spt = _subset_pools(w.k_pool, w.v_pool, pt, np.maximum(w.hist, 1), seqs, 16)
+    rows = np.concatenate([np.arange(s * P, (s + 1) * P) for s in seqs])
+    q_bits, k_bits, v_bits = host_bits(w.q)[rows], host_bits(w.k)[rows], host_bits(w.v)[rows]
+    ref = orc.paged_attention_prefill(q_bits, k_bits, v_bits, kb, vb, spt, w.hist[seqs], "bf16")
+    for i, s in enumerate(seqs):
+        got = out_h[s * P * hq:(s + 1) * P * hq]
+        assert_close(got, ref[i * P * hq:(i + 1) * P * hq], "bf16", f"reference signature seq {s} (history {int(w.hist[s])})")
