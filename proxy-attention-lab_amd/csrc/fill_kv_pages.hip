@@ -13,7 +13,8 @@
 //
 // Design (MI355X): HBM-bound byte movement, so the mapping is chosen for
 // whole-line writes and short dependency chains.  Workgroup (w, h) owns a
-// window of 64 consecutive new tokens (16 for small batches) and kv head h.
+// window of 64 consecutive new tokens (16 for small batches) and kv head h,
+// K and V both (twice the bytes in flight per destination lookup).
 // Its threads issue all their source loads first; meanwhile the first
 // threads resolve every token's destination (page, slot) into LDS.
 //  * K: a token's 8-dim chunk is one 16-byte stripe (16-bit pools) or half of
@@ -47,7 +48,7 @@ PAL_DEBUG_FLAGS_DEFINE(fill_debug_flags)
 namespace {
 
 #ifndef PAL_FILL_THREADS
-#define PAL_FILL_THREADS 256
+#define PAL_FILL_THREADS 512  // eight wavefronts: fewer source chunks (registers) per thread
 #endif
 constexpr int kThreads = PAL_FILL_THREADS;
 #ifndef PAL_FILL_LARGE_WIN
@@ -238,21 +239,21 @@ __device__ __forceinline__ void rotate_unit(const FillParams& p, int c0, int c1,
 // Workgroup (w, y) of the grid: y < Hkv moves K and V of kv head y for the
 // window of WIN new tokens w * WIN ..; y >= Hkv (rope with queries only)
 // rotates and casts query head y - Hkv of the window.  Each thread first
-// issues the loads of all its source chunks, chunks fastest so that a
-// wavefront reads whole lines of the source rows; meanwhile the first
-// wavefront resolves the destinations and classifies the window's tokens:
-// a token inside a full run of 8 slots of one page, or a single token.  A
-// single token's K chunks and V values are stored straight from registers.
-// Run tokens' rows go through LDS, and each run is then written in whole
-// lines: K stripe q of its 8 slots (8 x 16
-// contiguous bytes) and V row d of its 8 slots, the two runs of one page
-// side by side in neighbouring lanes.
+// issues the loads of all its source chunks, K and V, chunks fastest so that
+// a wavefront reads whole lines of the source rows; meanwhile the first
+// wavefront resolves the destinations (once for both) and classifies the
+// window's tokens: a token inside a full run of 8 slots of one page, or a
+// single token.  A single token's K chunks and V values are stored straight
+// from registers.  Run tokens' rows go through LDS, and each run is then
+// written in whole lines: K stripe q of its 8 slots (8 x 16 contiguous
+// bytes) and V row d of its 8 slots, the two runs of one page side by side
+// in neighbouring lanes.
 template <int SRC, int DST, int WIN, int MAXC>
 __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParams p) {
   constexpr int kItems = (WIN * MAXC + kThreads - 1) / kThreads;  // source chunks per thread, at most
   constexpr int EB = elem_bytes<DST>();
   static_assert(WIN <= kWave, "the first wavefront classifies the window");
-  // dynamic LDS: the run tokens' K or V rows, [WIN][HD * EB + kRowPad] bytes
+  // dynamic LDS: the run tokens' K rows, then their V rows, [2][WIN][HD * EB + kRowPad] bytes
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
   __shared__ uint32_t page_lds[WIN];  // destination page of each window token
   __shared__ int slot_lds[WIN];       // its slot, or -1: no valid destination
@@ -269,10 +270,10 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
   const int nwin = static_cast<int>(min(static_cast<int64_t>(WIN), p.num_tokens - t0));
   const int units = k_units(p);
 
-  if (static_cast<int>(blockIdx.y) >= 2 * p.num_kv_heads) {
+  if (static_cast<int>(blockIdx.y) >= p.num_kv_heads) {
     // ---- queries: rotate and cast head qh of the window's rows (a row is
     // contiguous in and out, so units run fastest: whole lines per wave)
-    const int qh = blockIdx.y - 2 * p.num_kv_heads;
+    const int qh = blockIdx.y - p.num_kv_heads;
     const int64_t q_row = static_cast<int64_t>(p.num_q_heads) * hd;
     Raw8<SRC> rx[kItems], ry[kItems];
     int pos[kItems];
@@ -312,32 +313,29 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
     return;
   }
 
-  // K workgroups (y < Hkv) and V workgroups (Hkv <= y < 2 Hkv) of kv head h
-  const bool is_k = static_cast<int>(blockIdx.y) < p.num_kv_heads;
-  const int h = is_k ? blockIdx.y : blockIdx.y - p.num_kv_heads;
+  // K and V of kv head h = y (y < Hkv)
+  const int h = blockIdx.y;
   const int64_t k_row = static_cast<int64_t>(p.num_kv_heads) * hd;  // source elements per token
   const int krow_bytes = hd * EB;                                    // one token's K or V row
   const int lrow = krow_bytes + kRowPad;                             // its LDS row stride
   uint8_t* k_lds = dyn_lds;
-  uint8_t* v_lds = dyn_lds;
-  // ---- issue every source load of this thread (K units or V chunks; chunks fastest)
-  Raw8<SRC> kx[kItems], ky[kItems];
+  uint8_t* v_lds = dyn_lds + WIN * lrow;
+  // ---- issue every source load of this thread: K units and V chunks of the
+  // window's rows (units / chunks fastest, so a wavefront reads whole lines)
+  Raw8<SRC> kx[kItems], ky[kItems], vx[kItems];
 #pragma unroll
   for (int k = 0; k < kItems; ++k) {
     const int it = tid + k * kThreads;
-    if (is_k) {
-      const int i = it / units;
-      if (i < nwin) {
-        int c0, c1;
-        unit_chunks(p, it % units, c0, c1);
-        const int64_t row = (t0 + i) * k_row + static_cast<int64_t>(h) * hd;
-        kx[k].load(p.new_k, row + 8 * c0);
-        if (c1 >= 0) ky[k].load(p.new_k, row + 8 * c1);
-      }
-    } else {
-      const int i = it / chunks;
-      if (i < nwin) kx[k].load(p.new_v, (t0 + i) * k_row + static_cast<int64_t>(h) * hd + 8 * (it % chunks));
+    const int i = it / units;
+    if (i < nwin) {
+      int c0, c1;
+      unit_chunks(p, it % units, c0, c1);
+      const int64_t row = (t0 + i) * k_row + static_cast<int64_t>(h) * hd;
+      kx[k].load(p.new_k, row + 8 * c0);
+      if (c1 >= 0) ky[k].load(p.new_k, row + 8 * c1);
     }
+    const int iv = it / chunks;
+    if (iv < nwin) vx[k].load(p.new_v, (t0 + iv) * k_row + static_cast<int64_t>(h) * hd + 8 * (it % chunks));
   }
   // ---- destinations (two dependent loads: the map, then the page table)
   if (tid < WIN) {
@@ -402,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
 #pragma unroll
   for (int k = 0; k < kItems; ++k) {
     const int it = tid + k * kThreads;
-    if (is_k) {  // K unit
+    {  // K unit
       const int i = it / units;
       if (i < nwin && slot_lds[i] >= 0) {
         int c0, c1;
@@ -432,7 +430,8 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
           if (c1 >= 0) *reinterpret_cast<typename Store8<DST>::T*>(k_lds + i * lrow + c1 * 8 * EB) = b;
         }
       }
-    } else {  // V chunk
+    }
+    {  // V chunk
       const int i = it / chunks;
       const int c = it % chunks;
       if (i < nwin && slot_lds[i] >= 0) {
@@ -440,10 +439,10 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
         uint32_t e16[8];
         if constexpr (SRC == DST) {  // bit copy
 #pragma unroll
-          for (int e = 0; e < 8; ++e) e16[e] = (kx[k].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          for (int e = 0; e < 8; ++e) e16[e] = (vx[k].w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
         } else {
           float x[8];
-          kx[k].to_f32(x);
+          vx[k].to_f32(x);
           if constexpr (DST == kFP8) {
             const u32x2 q = Store8<kFP8>::pack(x, vs_lds[i]);
 #pragma unroll
@@ -482,23 +481,20 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
 
   const int n_runs = n_runs_lds;
   if (n_runs == 0) return;
-  if (is_k) {
-    // ---- K of the runs: item = (stripe q, run r, slot j), slots fastest: 8
-    // lanes write the run's 128 contiguous bytes of stripe q (a stripe is 16
-    // bytes: 8 dims of 16-bit, 16 of fp8), and runs r, r+1 (often the two
-    // halves of one page) follow each other.
-    const int pieces = krow_bytes / 16;  // 16-byte pieces of a token's K row
-    for (int it = tid; it < pieces * n_runs * 8; it += kThreads) {
-      const int j = it % 8;
-      const int r = (it / 8) % n_runs;
-      const int q = it / (8 * n_runs);
-      const int i = run_lds[r] + j;
-      const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
-      // piece q is stripe q (16-bit: 8 dims, fp8: 16 dims) of the token
-      *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(p.k_pool) + hb + (static_cast<int64_t>(q) * tpp + slot_lds[i]) * 16) =
-          *reinterpret_cast<const u32x4*>(k_lds + i * lrow + q * 16);
-    }
-    return;
+  // ---- K of the runs: item = (stripe q, run r, slot j), slots fastest: 8
+  // lanes write the run's 128 contiguous bytes of stripe q (a stripe is 16
+  // bytes: 8 dims of 16-bit, 16 of fp8), and runs r, r+1 (often the two
+  // halves of one page) follow each other.
+  const int pieces = krow_bytes / 16;  // 16-byte pieces of a token's K row
+  for (int it = tid; it < pieces * n_runs * 8; it += kThreads) {
+    const int j = it % 8;
+    const int r = (it / 8) % n_runs;
+    const int q = it / (8 * n_runs);
+    const int i = run_lds[r] + j;
+    const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
+    // piece q is stripe q (16-bit: 8 dims, fp8: 16 dims) of the token
+    *reinterpret_cast<u32x4*>(static_cast<uint8_t*>(p.k_pool) + hb + (static_cast<int64_t>(q) * tpp + slot_lds[i]) * 16) =
+        *reinterpret_cast<const u32x4*>(k_lds + i * lrow + q * 16);
   }
   // ---- V of the runs: item = (row d, run r), runs fastest in pairs, so
   // lanes 2d, 2d+1 write row d of two runs (a page's two halves side by
@@ -536,8 +532,8 @@ hipError_t launch_win(const FillParams& p, hipStream_t stream) {
   // still spreads over 4 x 2 Hkv workgroups; prefill batches: 32
   const int win = p.num_tokens >= 2048 ? kLargeWin : kSmallWin;
   const int64_t windows = (p.num_tokens + win - 1) / win;
-  const unsigned gy = 2 * p.num_kv_heads + (p.q_in ? p.num_q_heads : 0);
-  const size_t lds = static_cast<size_t>(win) * (p.head_dim * elem_bytes<DST>() + kRowPad);  // K or V rows
+  const unsigned gy = p.num_kv_heads + (p.q_in ? p.num_q_heads : 0);
+  const size_t lds = 2 * static_cast<size_t>(win) * (p.head_dim * elem_bytes<DST>() + kRowPad);  // K and V rows
   if (win == kLargeWin)
     hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kLargeWin, MAXC>), dim3(static_cast<unsigned>(windows), gy),
                        dim3(kThreads), lds, stream, p);
