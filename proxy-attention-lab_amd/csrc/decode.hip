@@ -17,10 +17,8 @@
 //  * The global block list [0, T) is cut into "virtual workers": equal
 //    static ranges (one per resident wavefront), or, in the fixed-chunk mode
 //    (partition_size > 0), chunks of C blocks, each wavefront streaming a
-//    static run of consecutive chunks (when a static share below 1 is
-//    compiled in, a tail of chunks is claimed from an atomic counter
-//    instead).  Because the cut is fixed, which wavefront computes a chunk
-//    changes nothing in the result.
+//    static run of consecutive chunks.  Because the cut is fixed, which
+//    wavefront computes a chunk changes nothing in the result.
 //  * Each workgroup scans the sequence lengths into LDS (batches of up to
 //    1024 sequences; larger ones are scanned once by decode_plan_kernel into
 //    the workspace) and locates the sequence of a range by binary search.
@@ -69,11 +67,6 @@ constexpr int kGroupThreads = kWorkersPerGroup * kWave;
 constexpr int kPlanThreads = 1024;
 constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each workgroup
 constexpr int64_t kMergeGroups = 2048;  // merge grid (at most): workgroups stride over the list
-#ifndef PAL_DECODE_STATIC_SHARE
-#define PAL_DECODE_STATIC_SHARE 4  // static quarters of the block list (4 = all static)
-#endif
-constexpr int64_t kStaticShareNum = PAL_DECODE_STATIC_SHARE;
-constexpr int64_t kStaticShareDen = 4;
 
 struct Item {
   int64_t row;  // query / output row
@@ -110,10 +103,15 @@ __device__ __forceinline__ Item item_at(const DecodeParams& p, int64_t i, int tp
 }
 
 // The fixed cut of the global block list into virtual workers.
+// Equal shares: [0, T) split evenly over nws = min(resident workers, T)
+// virtual workers (none empty).  Fixed chunks: nc chunks of `chunk` blocks,
+// virtual ids nws + k with nws = 0.  (A dynamically claimed tail of chunks
+// after static shares measured much slower: each claimed range restarts the
+// load pipeline and writes its own partials.)
 struct Sched {
   int64_t total;  // T: blocks of all segments
   int64_t ts;     // static region [0, ts), split evenly over nws workers
-  int64_t nws;    // static virtual workers: min(resident workers, ts), so none is empty
+  int64_t nws;    // static virtual workers
   int64_t chunk;  // blocks per chunk
   int64_t nc;     // chunks covering [ts, total); virtual ids nws .. nws + nc - 1
 };
@@ -121,30 +119,18 @@ struct Sched {
 __device__ __forceinline__ Sched make_sched(int64_t total, int64_t nw, int tokens_per_worker) {
   Sched sc;
   sc.total = total;
-  if constexpr (kStaticShareNum == kStaticShareDen) {
-    if (tokens_per_worker <= 0) {  // equal shares only: no division on the start-up path
-      sc.ts = total;
-      sc.chunk = 1;
-      sc.nws = total < nw ? total : nw;
-      sc.nc = 0;
-      return sc;
-    }
+  if (tokens_per_worker <= 0) {  // equal shares: no division on the start-up path
+    sc.ts = total;
+    sc.chunk = 1;
+    sc.nws = total < nw ? total : nw;
+    sc.nc = 0;
+    return sc;
   }
-  if (tokens_per_worker > 0) {  // fixed-size chunks only (the reference's CHUNK_SIZE mode)
-    sc.ts = 0;
-    sc.chunk = tokens_per_worker / 16 > 0 ? tokens_per_worker / 16 : 1;
-  } else {
-    // Static shares only.  (A dynamically claimed tail would absorb the
-    // uneven finish of the shares, but each claimed range restarts the load
-    // pipeline and writes its own partials; small chunks cost more than
-    // they balance.)
-    sc.ts = total * kStaticShareNum / kStaticShareDen;
-    const int64_t dyn = total - sc.ts;
-    sc.chunk = (dyn + 4 * nw - 1) / (4 * nw);  // about four chunks per worker
-    if (sc.chunk < 1) sc.chunk = 1;
-  }
-  sc.nws = sc.ts < nw ? sc.ts : nw;
-  sc.nc = (total - sc.ts + sc.chunk - 1) / sc.chunk;
+  // fixed-size chunks (the reference's CHUNK_SIZE mode)
+  sc.ts = 0;
+  sc.chunk = tokens_per_worker / 16 > 0 ? tokens_per_worker / 16 : 1;
+  sc.nws = 0;
+  sc.nc = (total + sc.chunk - 1) / sc.chunk;
   return sc;
 }
 
@@ -760,15 +746,6 @@ __device__ __forceinline__ void stream_body(const DecodeParams& p, int64_t* cum_
     if (va < vb) process_range<DT, HD, TPP, PF, true, KV8>(p, sc, cum, il, n_items, va, vb);
   } else {
     if (w < sc.nws) process_range<DT, HD, TPP, PF, false, KV8>(p, sc, cum, il, n_items, w, w + 1);
-    if constexpr (kStaticShareNum < kStaticShareDen) {  // a dynamically claimed tail is compiled in
-      while (sc.nc > 0) {
-        uint32_t k = 0;
-        if (lane_id() == 0) k = atomicAdd(p.claim, 1u);
-        k = __builtin_amdgcn_readfirstlane(k);
-        if (k >= sc.nc) break;
-        process_range<DT, HD, TPP, PF, false, KV8>(p, sc, cum, il, n_items, sc.nws + k, sc.nws + k + 1);
-      }
-    }
   }
 }
 
@@ -1224,8 +1201,7 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
 // workers (it then fits the GPU in one round).
 template <int DT, int HD, int TPP>
 hipError_t launch_merge(const DecodeParams& p, hipStream_t stream) {
-  const bool all_static = p.tokens_per_worker == 0 && kStaticShareNum == kStaticShareDen;
-  int64_t merge_groups = all_static ? p.num_workers : kMergeGroups;
+  int64_t merge_groups = p.tokens_per_worker == 0 ? p.num_workers : kMergeGroups;
   if (merge_groups > p.list_cap) merge_groups = p.list_cap;
   hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(merge_groups)),
                      dim3(kGroupThreads), 0, stream, p);
@@ -1420,8 +1396,7 @@ int64_t decode_virtual_workers(int64_t resident, int64_t max_blocks, int partiti
     const int64_t chunk = partition_size / 16;
     return resident + (max_blocks + chunk - 1) / chunk;
   }
-  if (kStaticShareNum == kStaticShareDen) return resident + 1;  // equal static shares only
-  return 5 * resident + 1;  // static shares plus about four claimed chunks per worker
+  return resident + 1;  // equal static shares
 }
 
 hipError_t launch_decode(const DecodeParams& p, int dtype, int head_dim, int tokens_per_page, hipStream_t stream) {
