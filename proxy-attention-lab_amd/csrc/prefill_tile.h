@@ -61,6 +61,7 @@ constexpr int kMRows = kPfWaves * 32;  // M-rows (token, head) per workgroup
 constexpr int kKeys = 32;              // keys per step
 constexpr int kNBuf = 4;               // LDS step buffers (read by stragglers, computed, two in flight)
 constexpr int kPidChunk = 512;         // page ids staged per chunk; two chunks live in LDS
+static_assert(kPidChunk % kPfThreads == 0, "a page-id chunk is a whole number of loads per thread");
 constexpr float kLazyRescale = 8.f;    // log2 headroom before the running max moves
 
 // A step moves 4*HD items of 16 bytes of K and as many of V.
@@ -177,6 +178,34 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     slen = slen < 0 ? 0 : (slen > max_tokens ? max_tokens : slen);
   }
 
+  // Loads that need nothing but the tile's coordinates go out first, so
+  // their latency overlaps the row-limit round trip: the query operand and
+  // the first kPidChunk page-table entries of the row (staged into LDS once
+  // the limits say how many the tile reads; entries past the sequence's
+  // pages are never used).
+  const int m_row = w * 32 + col;  // this lane's M-row
+  const int my_t = m_row / p.hg_max;
+  const int my_h = m_row % p.hg_max;
+  const bool row_ok = my_t < nrows && my_t < qt && my_h < hg;
+  // Q^T operand: lane holds Q[M-row col][16kk + 8 half .. +7] for all k-steps.
+  u32x4 qv[KS];
+  {
+    const int64_t qrow = static_cast<int64_t>(row0 + (row_ok ? my_t : 0)) * p.num_q_heads + kvh * p.group + h0 +
+                         (row_ok ? my_h : 0);
+    const uint16_t* qp = p.q + qrow * HD + 8 * half;
+    const uint32_t qmask = row_ok ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qv[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk) & qmask;
+  }
+  const uint32_t* pt = p.page_table + s * p.page_table_width;
+  constexpr int kPidPre = kPidChunk / kPfThreads;  // entries of chunk 0 per thread
+  uint32_t pid_pre[kPidPre];
+#pragma unroll
+  for (int j = 0; j < kPidPre; ++j) {
+    const int e = tid + j * kPfThreads;
+    pid_pre[j] = e < p.page_table_width ? pt[e] : 0u;
+  }
+
   // Row limits: M-row m = token * hg_max + head.  The previous tile's last
   // reads of the min / max words passed a barrier since.
   if (tid == 0) {
@@ -204,28 +233,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // words after the per-row limits, reset before the first barrier above)
   const int max_lim = __builtin_amdgcn_readfirstlane(lim_lds[kMRows]);
   const int min_lim = __builtin_amdgcn_readfirstlane(lim_lds[kMRows + 1]);
-  const int m_row = w * 32 + col;  // this lane's M-row
-  const int my_t = m_row / p.hg_max;
-  const int my_h = m_row % p.hg_max;
-  const bool row_ok = my_t < nrows && my_t < qt && my_h < hg;
   const int my_lim = lim_lds[m_row];
-
-  // Q^T operand: lane holds Q[M-row col][16kk + 8 half .. +7] for all k-steps.
-  u32x4 qv[KS];
-  {
-    const int64_t qrow = static_cast<int64_t>(row0 + (row_ok ? my_t : 0)) * p.num_q_heads + kvh * p.group + h0 +
-                         (row_ok ? my_h : 0);
-    const uint16_t* qp = p.q + qrow * HD + 8 * half;
-    const uint32_t qmask = row_ok ? 0xFFFFFFFFu : 0u;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qv[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk) & qmask;
-  }
 
   const int64_t head_block = static_cast<int64_t>(HD) * TPP;
   const int64_t page_stride = head_block * p.num_kv_heads;
   const int64_t page_stride8 = page_stride;            // fp8 pools: bytes per page (one byte per element)
   const int64_t kv_head_off8 = kvh * head_block;       // and of a kv head's block
-  const uint32_t* pt = p.page_table + s * p.page_table_width;
   const int64_t dense_row0 = s * p.prompt_len - hist;  // dense row of key token tok: dense_row0 + tok
   const int64_t dense_stride = static_cast<int64_t>(p.num_kv_heads) * HD;
   const int64_t kv_head_off = kvh * head_block;
@@ -529,7 +542,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // and the PV MFMAs of step st beside the exp-sum of step st and the row max
   // of step st+1, which gives the next iteration its exponent offset.
   if (nsteps > 0) {
-    stage_pids(0);
+#pragma unroll
+    for (int j = 0; j < kPidPre; ++j) {  // chunk 0, loaded above
+      const int e = tid + j * kPfThreads;
+      if (e < n_pid) pid_lds[e] = pid_pre[j];
+    }
     if (n_pid > kPidChunk) stage_pids(1);
   }
   __syncthreads();
