@@ -256,12 +256,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       pid_lds[e % (2 * kPidChunk)] = pt[e];
   };
 
-  // Fast step: all 32 keys below the tile's largest limit, in valid pages
-  // (and, in prompt mode, below the history): one direct-to-LDS copy per item,
-  // no registers, nothing to wait for here.  Every wavefront issues exactly
+  // Fast step: its first key below the tile's largest limit (the last step
+  // may end past it), in valid pages (and, in prompt mode, all 32 keys below
+  // the history, or all of them prompt keys): one direct-to-LDS copy per
+  // item, no registers, nothing to wait for here.  Every wavefront issues exactly
   // 2*NL copies (items past the step go to a junk slot), so the wait counts
   // are the same on every wavefront.
-  // Slow step (tile end, invalid pages, history / prompt boundary, fp8): register loads,
+  // Slow step (invalid pages, history / prompt boundary, fp8): register loads,
   // masked, then LDS stores -- synchronous, so it also drains the copies in
   // flight, which keeps the counted waits safe.
   // pg0 / pg1: the pages of the step's first and (TPP 16) second 16 keys.
