@@ -1001,7 +1001,7 @@ void fused_kernel(const DecodeParams dp, const PrefillParams pp, const unsigned 
   if (blockIdx.x < n_dec)
     fused_decode_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), KV8>(dp, lds.d);
   else
-    prefill_block<DT, HD, TPP, KV8>(pp, blockIdx.x - n_dec, lds.f);
+    prefill_block<DT, HD, TPP, KV8, false>(pp, blockIdx.x - n_dec, lds.f);
 }
 
 // Walks the merge list, slot v for virtual worker v (first block < 0:

@@ -590,8 +590,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // the unmasked body.  The last step is always in the masked part, whose
   // mask also discards the scores of the stale buffer it reads as "next".
   const int n_main = max(0, min(nsteps, min_lim / kKeys - 1));
-  auto step = [&](auto masked, int st) {
+  // dense_v: step st's V rows were copied untransposed (a dense prompt step);
+  // each combination is its own loop body, so the operand reads carry no
+  // per-chunk branch.
+  auto step = [&](auto masked, auto dense_v, int st) {
     constexpr bool kMask = decltype(masked)::value;
+    constexpr bool vdense = decltype(dense_v)::value;
     wait_barrier(st + 2 < nsteps ? 1 : 0);  // step st+1 has landed
     const int j = st + 3;
     const u32x2 pgv = read_pids(j);  // used after the MFMAs (in bounds whether or not step j exists)
@@ -614,7 +618,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // issues MFMAs (measured +1 % on config 4, -1 to -3 % time on config 5).
     __builtin_amdgcn_s_setprio(1);
     const int vbuf = st % kNBuf;
-    const bool vdense = is_dense(st);  // step st's V rows were copied untransposed
     f32x16 s_next;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
@@ -623,7 +626,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       s_next = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_next);
-      if (vdense) {
+      if constexpr (vdense) {
         // raw rows: V[key][d] in chunk (d / 8) ^ vd_swz(key) of row key.  Lane
         // 4r + c of a 16-lane group points at keys kg + 4t + r, dims d0 + 4c ..
         // +3 (d0 = 32 (kk % DT32) + (col & 16)); the transposing read hands
@@ -689,9 +692,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     }
     s_cur = s_next;
   };
+  // prompt mode: steps from ceil(hist / 32) on are dense (the one across the
+  // boundary, if any, is not)
+  const int fd = PROMPT ? min(nsteps, static_cast<int>((hist + kKeys - 1) / kKeys)) : nsteps;
   int st = 0;
-  for (; st < n_main; ++st) step(std::false_type{}, st);
-  for (; st < nsteps; ++st) step(std::true_type{}, st);
+  for (; st < min(n_main, fd); ++st) step(std::false_type{}, std::false_type{}, st);
+  if constexpr (PROMPT)
+    for (; st < n_main; ++st) step(std::false_type{}, std::true_type{}, st);
+  for (; st < fd; ++st) step(std::true_type{}, std::false_type{}, st);
+  if constexpr (PROMPT)
+    for (; st < nsteps; ++st) step(std::true_type{}, std::true_type{}, st);
 
   // ---- normalise and write: lane holds O[M-row col][32n + 8(r/4) + 4 half + r%4]
   float l = sum_xor32(l_run);
@@ -742,7 +752,9 @@ struct PrefillLds {
 //    last window first (rows of a sequence usually come in position order,
 //    so its later windows see more keys); every run of rows of one sequence
 //    inside the window that is not a lone decode row is computed as a tile.
-template <int DT, int HD, int TPP, bool KV8>
+// kPromptMode false: the caller never runs the uniform-prompt mode (the
+// fused kernel), which is then not compiled in.
+template <int DT, int HD, int TPP, bool KV8, bool kPromptMode = true>
 __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned block, PrefillLds<HD>& L) {
   uint16_t* k_lds = L.k;
   uint16_t* v_lds = L.v;
@@ -756,14 +768,16 @@ __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned b
   const int kvh = g / p.head_chunks;
   const int h0 = (g % p.head_chunks) * 16;
   const int qt = kMRows / p.hg_max;
-  if (p.prompt_len > 0) {
-    const int tps = (p.prompt_len + qt - 1) / qt;
-    const int s = unit / tps;
-    const int j = tps - 1 - (unit - s * tps);
-    const int row0 = s * p.prompt_len + j * qt;
-    prefill_tile<DT, HD, TPP, true, KV8>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds, junk_lds,
-                                    pid_lds, lim_lds);
-    return;
+  if constexpr (kPromptMode) {
+    if (p.prompt_len > 0) {
+      const int tps = (p.prompt_len + qt - 1) / qt;
+      const int s = unit / tps;
+      const int j = tps - 1 - (unit - s * tps);
+      const int row0 = s * p.prompt_len + j * qt;
+      prefill_tile<DT, HD, TPP, true, KV8>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds,
+                                           junk_lds, pid_lds, lim_lds);
+      return;
+    }
   }
   // windows in reverse row order: a sequence's later rows see more keys, so
   // its longest tiles start first and the grid ends on short ones
