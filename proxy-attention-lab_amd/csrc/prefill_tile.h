@@ -657,7 +657,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // after the chunks); other steps take the synchronous path below.
     const uint32_t jp0 = __builtin_amdgcn_readfirstlane(pgv.x);
     const uint32_t jp1 = TPP == 16 ? __builtin_amdgcn_readfirstlane(pgv.y) : jp0;
-    const bool jdense = j < nsteps && is_dense(j);
+    const bool jdense = j < nsteps && (vdense || is_dense(j));  // steps after a dense one are dense
     const bool jfast = j < nsteps && (jdense || is_fast(j, jp0, jp1));
     const int64_t joff0 = static_cast<int64_t>(jp0) * page_stride + kv_head_off;
     const int64_t joff1 = static_cast<int64_t>(jp1) * page_stride + kv_head_off;
