@@ -996,7 +996,7 @@ __global__ __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2
 void fused_kernel(const DecodeParams dp, const PrefillParams pp, const unsigned n_dec) {
   __shared__ union {
     FusedDecodeLds d;
-    PrefillLds<HD> f;
+    PrefillLds<HD, KV8> f;
   } lds;
   if (blockIdx.x < n_dec)
     fused_decode_body<DT, HD, TPP, shared_cu_prefetch<HD, TPP>(), KV8>(dp, lds.d);

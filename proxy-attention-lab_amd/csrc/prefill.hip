@@ -27,12 +27,12 @@ namespace {
 template <int DT, int HD, int TPP, bool KV8>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_tile_kernel(const PrefillParams p) {
-  __shared__ PrefillLds<HD> lds;
+  __shared__ PrefillLds<HD, KV8> lds;
   prefill_block<DT, HD, TPP, KV8>(p, blockIdx.x, lds);
 }
 template <int DT, int HD, int TPP, bool KV8>
 __global__ __launch_bounds__(kPfThreads) void prefill_tile_kernel_wide(const PrefillParams p) {
-  __shared__ PrefillLds<HD> lds;
+  __shared__ PrefillLds<HD, KV8> lds;
   prefill_block<DT, HD, TPP, KV8>(p, blockIdx.x, lds);
 }
 

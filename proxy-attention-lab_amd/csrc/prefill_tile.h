@@ -138,7 +138,7 @@ struct ItemMap {
 template <int DT, int HD, int TPP, bool PROMPT, bool KV8>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, int nrows, int64_t s, int kvh, int h0,
                                              uint16_t* k_lds_base, uint16_t* v_lds_base, uint16_t* junk_lds,
-                                             uint32_t* pid_lds, int* lim_lds) {
+                                             uint32_t* pid_lds, int* lim_lds, float* scl_lds) {
   static_assert(HD % 32 == 0, "prefill needs head_dim % 32 == 0");
   static_assert(2 * StepGeo<HD>::kLoads <= HD / 16, "a step's copies fit in its PV chunks");
   constexpr int KS = HD / 16;  // QK k-steps of 16
@@ -146,6 +146,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   constexpr int NI = StepGeo<HD>::kItems;
   constexpr int NL = StepGeo<HD>::kLoads;
   using IM = ItemMap<HD, TPP>;
+  // fp8 pools in window mode: steps are copied as fp8 bytes (16-byte items:
+  // 16 dims of one key for K, 16 keys of one row for V; 2 HD items each, in
+  // item order) and converted in the operand reads.  A copy instruction must
+  // stay in one page: with TPP 16 that needs HD % 64 == 0 (every fp8 pool's
+  // head dim).
+  constexpr bool F8 = KV8 && !PROMPT && (TPP == 32 || HD % 64 == 0);
+  constexpr int NI8 = 2 * HD;
+  constexpr int NL8 = (NI8 + kPfThreads - 1) / kPfThreads;
+  constexpr int NC = F8 ? NL8 : NL;  // copies per thread per step, K (and V)
+  float* ks_lds = scl_lds;                   // fp8: K scale of page-table entry e in slot e % 1024
+  float* vs_lds = scl_lds + 2 * kPidChunk;   // and V scale
   auto k_lds = [&](int b) { return k_lds_base + b * NI * 8; };
   auto v_lds = [&](int b) { return v_lds_base + b * NI * 8; };
 
@@ -228,6 +239,21 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       atomicMin(&lim_lds[kMRows + 1], lim);
     }
   }
+  // fp8: the scales of those page-table entries, behind the page ids
+  float ks_pre[kPidPre], vs_pre[kPidPre];
+#pragma unroll
+  for (int j = 0; j < kPidPre; ++j) {
+    ks_pre[j] = 0.f;
+    vs_pre[j] = 0.f;
+    if constexpr (F8) {
+      const int e = tid + j * kPfThreads;
+      if (e < p.page_table_width && pid_pre[j] < p.num_pages) {
+        const int64_t si = static_cast<int64_t>(pid_pre[j]) * p.num_kv_heads + kvh;
+        ks_pre[j] = p.k_scales[si];
+        vs_pre[j] = p.v_scales[si];
+      }
+    }
+  }
   __syncthreads();
   // largest and smallest limit over the tile's rows (LDS atomics, two
   // words after the per-row limits, reset before the first barrier above)
@@ -251,9 +277,22 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // Page ids live in LDS (two chunks of 512 entries, entry e in slot e % 1024):
   // reading them is an LDS broadcast, so the only vector-memory traffic in the
   // step loop is the K/V copies, whose count the waits below rely on.
+  // fp8: the (page, kv head) scales of entry e, beside its page id (0 for an
+  // invalid id: such a step takes the register path, which reads none)
+  auto stage_scales = [&](int e, uint32_t pg) {
+    if constexpr (F8) {
+      const bool ok = pg < p.num_pages;
+      const int64_t si = static_cast<int64_t>(ok ? pg : 0) * p.num_kv_heads + kvh;
+      ks_lds[e % (2 * kPidChunk)] = ok ? p.k_scales[si] : 0.f;
+      vs_lds[e % (2 * kPidChunk)] = ok ? p.v_scales[si] : 0.f;
+    }
+  };
   auto stage_pids = [&](int chunk) {  // synchronous; callers hold a barrier after it
-    for (int e = chunk * kPidChunk + tid; e < min((chunk + 1) * kPidChunk, n_pid); e += kPfThreads)
-      pid_lds[e % (2 * kPidChunk)] = pt[e];
+    for (int e = chunk * kPidChunk + tid; e < min((chunk + 1) * kPidChunk, n_pid); e += kPfThreads) {
+      const uint32_t pg = pt[e];
+      pid_lds[e % (2 * kPidChunk)] = pg;
+      stage_scales(e, pg);
+    }
   };
 
   // Fast step: its first key below the tile's largest limit (the last step
@@ -290,13 +329,98 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       copy_to_lds16(page, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
     }
   };
-  // step j takes the fast path (fp8 pools take the register path: the
-  // copies cannot dequantize)
+  // fp8 items.  K item i: page half ph (TPP 16), stripe c (dims 16c ..
+  // 16c+15), key of the step; V item i: page half ph (TPP 16) or 16-key half
+  // of the page row (TPP 32), row d.  Item i is LDS slot i.
+  auto k8_item = [](int i, int& ph, int& c, int& key) {
+    if (TPP == 16) {
+      ph = i / HD;
+      c = (i % HD) / 16;
+      key = 16 * ph + i % 16;
+    } else {
+      ph = 0;
+      c = i / 32;
+      key = i % 32;
+    }
+  };
+  auto v8_item = [](int i, int& ph, int& d, int& kb) {  // kb: the item's first key in the step
+    if (TPP == 16) {
+      ph = i / HD;
+      d = i % HD;
+      kb = 16 * ph;
+    } else {
+      ph = 0;
+      d = i / 2;
+      kb = 16 * (i % 2);
+    }
+  };
+  const uint8_t* k8_pool = reinterpret_cast<const uint8_t*>(p.k_pool) + kv_head_off8;
+  const uint8_t* v8_pool = reinterpret_cast<const uint8_t*>(p.v_pool) + kv_head_off8;
+  // Copy q of an fp8 fast step: K items (q < NL8) or V items of load q % NL8;
+  // boff0 / boff1: byte offsets of the step's two pages' blocks.
+  auto copy8 = [&](int q, int buf, int64_t boff0, int64_t boff1) {
+    const int jj = q % NL8;
+    const int i = tid + jj * kPfThreads;
+    const int ib = w * kWave + jj * kPfThreads;  // first item of this wavefront's load
+    const bool ok = ib < NI8;
+    int ph = 0, a = 0, b = 0;
+    uint32_t src = 0;
+    if (q < NL8) {
+      if (ok) k8_item(i, ph, a, b);
+      src = static_cast<uint32_t>((a * TPP + b % TPP) * 16);
+    } else {
+      if (ok) v8_item(i, ph, a, b);
+      src = static_cast<uint32_t>(a * TPP + b % TPP);
+    }
+    const int phw = (TPP == 16 && ok) ? ib / HD : 0;  // the load's page half (one page per instruction)
+    const uint8_t* page = (q < NL8 ? k8_pool : v8_pool) + (phw ? boff1 : boff0);
+    copy_to_lds16(page, ok ? src : 0u, lds_addr(ok ? (q < NL8 ? k_lds(buf) : v_lds(buf)) + ib * 8 : junk_lds));
+  };
+  // An fp8 step on the register path (a page id out of range): the same
+  // items, zero for invalid pages, V keys past max_lim cleared.
+  auto slow8 = [&](int j, uint32_t pg0, uint32_t pg1) {
+    const int buf = j % kNBuf;
+    const int k0 = j * kKeys;
+#pragma unroll
+    for (int jj = 0; jj < NL8; ++jj) {
+      const int i = tid + jj * kPfThreads;
+      if (i >= NI8) continue;
+      {
+        int ph, c, key;
+        k8_item(i, ph, c, key);
+        const uint32_t pg = ph ? pg1 : pg0;
+        PAL_DEBUG_FLAG(pg >= p.num_pages && k0 + key < max_lim, kDebugPageId);
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (pg < p.num_pages && k0 + key < max_lim)
+          val = *reinterpret_cast<const u32x4*>(k8_pool + static_cast<int64_t>(pg) * page_stride8 +
+                                                (c * TPP + key % TPP) * 16);
+        *reinterpret_cast<u32x4*>(k_lds(buf) + i * 8) = val;
+      }
+      {
+        int ph, d, kb;
+        v8_item(i, ph, d, kb);
+        const uint32_t pg = ph ? pg1 : pg0;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        const int valid = max_lim - (k0 + kb);
+        if (pg < p.num_pages && valid > 0) {
+          val = *reinterpret_cast<const u32x4*>(v8_pool + static_cast<int64_t>(pg) * page_stride8 + d * TPP + kb % TPP);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+              if (4 * e + bb >= valid) val[e] &= ~(0xFFu << (8 * bb));
+        }
+        *reinterpret_cast<u32x4*>(v_lds(buf) + i * 8) = val;
+      }
+    }
+  };
+  // step j takes the fast path (fp8 pools only in window mode, as fp8 items;
+  // the 16-bit copies cannot dequantize)
   // (the tile's last step may end past max_lim: its copies then read keys
   // no row sees, from valid pages, and fix_tail clears their V entries)
   auto is_fast = [&](int j, uint32_t pg0, uint32_t pg1) {
     const int k0 = j * kKeys;
-    return !KV8 && k0 < max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
+    return (!KV8 || F8) && k0 < max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
   };
   // Prompt mode: a step whose 32 keys are all prompt keys below the tile's
   // largest limit copies them from the dense prompt rows (16-bit in every
@@ -346,6 +470,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     }
     if (TPP != 16) pg1 = pg0;
     const bool fast = is_fast(j, pg0, pg1);
+    if constexpr (F8) {
+      if (fast) {
+#pragma unroll
+        for (int q = 0; q < 2 * NL8; ++q)
+          copy8(q, buf, static_cast<int64_t>(pg0) * page_stride8, static_cast<int64_t>(pg1) * page_stride8);
+      } else {
+        slow8(j, pg0, pg1);
+      }
+      return;
+    }
     if (fast) {
       const int64_t off0 = static_cast<int64_t>(pg0) * page_stride + kv_head_off;
       const int64_t off1 = static_cast<int64_t>(pg1) * page_stride + kv_head_off;
@@ -447,6 +581,27 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   auto fix_tail = [&](int j) {
     const int valid0 = max_lim - j * kKeys;  // valid keys of the step, 1 .. 31
     uint16_t* vb = v_lds(j % kNBuf);
+    if constexpr (F8) {  // fp8 items: 16 key bytes of one row
+#pragma unroll
+      for (int jj = 0; jj < NL8; ++jj) {
+        const int i = tid + jj * kPfThreads;
+        if (i >= NI8) continue;
+        int ph, d, kb;
+        v8_item(i, ph, d, kb);
+        const int valid = valid0 - kb;
+        if (valid < 16) {
+          u32x4* slot = reinterpret_cast<u32x4*>(vb + i * 8);
+          u32x4 val = *slot;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+              if (4 * e + bb >= valid) val[e] &= ~(0xFFu << (8 * bb));
+          *slot = val;
+        }
+      }
+      return;
+    }
     const bool dense = is_dense(j);
 #pragma unroll
     for (int jj = 0; jj < NL; ++jj) {
@@ -471,6 +626,25 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   };
   const bool tail_partial = max_lim % kKeys != 0;  // the last step ends past max_lim
   // the page ids of step j (an LDS broadcast read; TPP 32: one page)
+  // fp8: the scales of step j's first and (TPP 16) second page (LDS
+  // broadcast); 0 for a page past the tile's last staged entry (the tail
+  // step's keys past max_lim: their V bytes are cleared, and 0 x a stale
+  // scale could be NaN)
+  auto read_scales = [&](const float* arr, int j, float& s0, float& s1) {
+    const int e = j * kKeys / TPP;
+    s0 = e < n_pid ? arr[e % (2 * kPidChunk)] : 0.f;
+    s1 = TPP == 16 ? (e + 1 < n_pid ? arr[(e + 1) % (2 * kPidChunk)] : 0.f) : s0;
+  };
+  // fp8: step j's scores times the K scale of each key's page (register r
+  // holds key 16 (r / 8) + ..., so r < 8: the first page)
+  auto scale_scores = [&](f32x16& sacc, int j) {
+    if constexpr (F8) {
+      float s0, s1;
+      read_scales(ks_lds, j, s0, s1);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] *= r < 8 ? s0 : s1;
+    }
+  };
   auto read_pids = [&](int j) {
     const int e = (j * kKeys / TPP) % (2 * kPidChunk);
     u32x2 v;
@@ -499,6 +673,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d] for step st (raw scores).
   auto read_k = [&](int st, u32x4 (&ka)[KS]) {
     const int buf = st % kNBuf;
+    if constexpr (F8) {  // lane: key kperm(col), 8 dims of stripe kk (exact in 16 bits; the scale goes on the scores)
+      const int key = kperm(col);
+      const uint8_t* kb = reinterpret_cast<const uint8_t*>(k_lds(buf));
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int slot = TPP == 16 ? (key / 16) * HD + kk * 16 + key % 16 : kk * 32 + key;
+        ka[kk] = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(kb + slot * 16 + 8 * half), 1.f);
+      }
+      return;
+    }
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       const int c = 2 * kk + half;  // stripe of dims 16kk + 8 half .. +7
@@ -546,7 +730,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int j = 0; j < kPidPre; ++j) {  // chunk 0, loaded above
       const int e = tid + j * kPfThreads;
-      if (e < n_pid) pid_lds[e] = pid_pre[j];
+      if (e < n_pid) {
+        pid_lds[e] = pid_pre[j];
+        if constexpr (F8) {
+          ks_lds[e] = ks_pre[j];
+          vs_lds[e] = vs_pre[j];
+        }
+      }
     }
     if (n_pid > kPidChunk) stage_pids(1);
   }
@@ -554,9 +744,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   auto wait_barrier = [&](int pending_steps) {  // all but the pending_steps youngest steps' copies landed
     compiler_fence();
     if (pending_steps >= 2)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NL));
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NC));
     else if (pending_steps == 1)
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NL));
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NC));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     __builtin_amdgcn_s_waitcnt(kLgkmZero);
@@ -578,6 +768,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     read_k(0, ka);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) s_cur = Dt<DT>::mma32x32x16(ka[kk], qv[kk], s_cur);
+    scale_scores(s_cur, 0);
     float bm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -618,6 +809,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // issues MFMAs (measured +1 % on config 4, -1 to -3 % time on config 5).
     __builtin_amdgcn_s_setprio(1);
     const int vbuf = st % kNBuf;
+    float vs0 = 1.f, vs1 = 1.f;  // fp8: V scales of step st's pages
+    if constexpr (F8) read_scales(vs_lds, st, vs0, vs1);
     f32x16 s_next;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
@@ -638,6 +831,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         const u32x2 lo = lds_read_tr16(vr);           // keys kg .. kg+3
         const u32x2 hi = lds_read_tr16(vr + 4 * HD);  // keys kg+4 .. kg+7 (vd_swz(key + 4) = vd_swz(key))
         va[kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else if constexpr (F8) {  // row d = col + 32 (kk % DT32), keys 16 g + 8 half .. +7 of item (g, d)
+        const int g = kk / DT32;
+        const int d = col + 32 * (kk % DT32);
+        const int slot = TPP == 16 ? g * HD + d : d * 2 + g;
+        va[kk] = fp8x8_scaled<DT>(
+            *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half),
+            (TPP == 16 && g) ? vs1 : vs0);
       } else {
         va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
       }
@@ -648,6 +848,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       sched_fence();
     }
     const u32x4 pb[2] = {u32x4{pp[0], pp[1], pp[2], pp[3]}, u32x4{pp[4], pp[5], pp[6], pp[7]}};
+    scale_scores(s_next, st + 1);
     // O^T[d][M-row] += sum_key V[key][d] P[M-row][key]; k-step kk takes
     // registers 8kk .. 8kk+7 = keys 16kk + 8 half .. +7.
     float bm = -INFINITY;
@@ -663,8 +864,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     const int64_t joff1 = static_cast<int64_t>(jp1) * page_stride + kv_head_off;
 #pragma unroll
     for (int m = 0; m < KS; ++m) {
-      if (jfast && m < 2 * NL) {
-        if (jdense)
+      if (jfast && m < 2 * NC) {
+        if constexpr (F8)
+          copy8(m, j % kNBuf, static_cast<int64_t>(jp0) * page_stride8, static_cast<int64_t>(jp1) * page_stride8);
+        else if (jdense)
           copy_dense(m, j % kNBuf, j);
         else
           copy_one(m, j % kNBuf, joff0, joff1);
@@ -732,12 +935,13 @@ __device__ __forceinline__ bool single_row(const uint32_t* q2seq, int64_t r, int
 // LDS of a prefill workgroup: four K and four V step buffers, the target of
 // padding copies, two chunks of page ids, the rows' key limits (with their
 // max and min) and the run starts of a window.
-template <int HD>
+template <int HD, bool KV8>
 struct PrefillLds {
   __attribute__((aligned(16))) uint16_t k[kNBuf * StepGeo<HD>::kItems * 8];
   __attribute__((aligned(16))) uint16_t v[kNBuf * StepGeo<HD>::kItems * 8];
   __attribute__((aligned(16))) uint16_t junk[kWave * 8];
   uint32_t pid[2 * kPidChunk];
+  float scl[KV8 ? 4 * kPidChunk : 1];  // fp8 pools: K then V scale of each staged page id
   int lim[kMRows + 2];
   int run_start[kMRows];
 };
@@ -755,11 +959,12 @@ struct PrefillLds {
 // kPromptMode false: the caller never runs the uniform-prompt mode (the
 // fused kernel), which is then not compiled in.
 template <int DT, int HD, int TPP, bool KV8, bool kPromptMode = true>
-__device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned block, PrefillLds<HD>& L) {
+__device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned block, PrefillLds<HD, KV8>& L) {
   uint16_t* k_lds = L.k;
   uint16_t* v_lds = L.v;
   uint16_t* junk_lds = L.junk;
   uint32_t* pid_lds = L.pid;
+  float* scl_lds = L.scl;
   int* lim_lds = L.lim;
   int* run_start = L.run_start;
   const int G = p.num_kv_heads * p.head_chunks;
@@ -775,7 +980,7 @@ __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned b
       const int j = tps - 1 - (unit - s * tps);
       const int row0 = s * p.prompt_len + j * qt;
       prefill_tile<DT, HD, TPP, true, KV8>(p, row0, min(qt, p.prompt_len - j * qt), s, kvh, h0, k_lds, v_lds,
-                                           junk_lds, pid_lds, lim_lds);
+                                           junk_lds, pid_lds, lim_lds, scl_lds);
       return;
     }
   }
@@ -793,7 +998,7 @@ __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned b
     end = __builtin_amdgcn_readfirstlane(end);
     if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
       prefill_tile<DT, HD, TPP, false, KV8>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
-                                       lim_lds);
+                                       lim_lds, scl_lds);
     cur = end;
   }
 }
