@@ -837,14 +837,22 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         const int slot = TPP == 16 ? g * HD + d : d * 2 + g;
         va[kk] = fp8x8_scaled<DT>(
             *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half),
-            (TPP == 16 && g) ? vs1 : vs0);
+            1.f);  // exact in 16 bits; the V scale is on P
       } else {
         va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
       }
 #pragma unroll
       for (int r = kk * 16 / KS; r < (kk + 1) * 16 / KS; ++r) pe[r] = __builtin_amdgcn_exp2f(pe[r]);
 #pragma unroll
-      for (int q = kk * 8 / KS; q < (kk + 1) * 8 / KS; ++q) pp[q] = Dt<DT>::pack2(pe[2 * q], pe[2 * q + 1]);
+      for (int q = kk * 8 / KS; q < (kk + 1) * 8 / KS; ++q) {
+        if constexpr (F8) {  // the exp-sum of the probabilities, then P times its key's page V scale
+          const float sv = (TPP == 16 && q >= 4) ? vs1 : vs0;
+          l_run += pe[2 * q] + pe[2 * q + 1];
+          pp[q] = Dt<DT>::pack2(pe[2 * q] * sv, pe[2 * q + 1] * sv);
+        } else {
+          pp[q] = Dt<DT>::pack2(pe[2 * q], pe[2 * q + 1]);
+        }
+      }
       sched_fence();
     }
     const u32x4 pb[2] = {u32x4{pp[0], pp[1], pp[2], pp[3]}, u32x4{pp[4], pp[5], pp[6], pp[7]}};
@@ -875,7 +883,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       o[m % DT32] = Dt<DT>::mma32x32x16(va[m], pb[m / DT32], o[m % DT32]);
       // the exp-sum adds the probabilities as rounded for the PV product
 #pragma unroll
-      for (int q = m * 8 / KS; q < (m + 1) * 8 / KS; ++q) l_run = Dt<DT>::sum2(pp[q], l_run);
+      for (int q = m * 8 / KS; q < (m + 1) * 8 / KS; ++q)
+        if constexpr (!F8) l_run = Dt<DT>::sum2(pp[q], l_run);
 #pragma unroll
       for (int r = m * 16 / KS; r < (m + 1) * 16 / KS; ++r) {
         if (kMask) mask_score(s_next, r, st + 1);
