@@ -150,6 +150,30 @@ struct Dt<kF16> {
   }
 };
 
+// Eight fp8 e4m3 values (w: bytes 0..7) as packed 16-bit values of dtype DT,
+// exactly (every e4m3 value, subnormals and NaN included, is a bf16 and an
+// fp16 value): one v_cvt_scalef32_pk_* per pair, with scale 1.
+template <int DT>
+__device__ __forceinline__ u32x4 fp8x8_exact(u32x2 w) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t word = q < 2 ? w.x : w.y;
+    if constexpr (DT == kBF16) {
+      const bf16x2_t v = (q & 1) ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.f, true)
+                                 : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.f, false);
+      r[q] = __builtin_bit_cast(uint32_t, v);
+    } else {
+      const f16x2_t v = (q & 1) ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.f, true)
+                                : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.f, false);
+      r[q] = __builtin_bit_cast(uint32_t, v);
+    }
+  }
+  return r;
+}
+
 // Eight fp8 e4m3 values (w: bytes 0..7) times scale s, as packed 16-bit
 // values of dtype DT (round to nearest even).
 template <int DT>

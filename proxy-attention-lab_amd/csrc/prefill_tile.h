@@ -679,7 +679,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
         const int slot = TPP == 16 ? (key / 16) * HD + kk * 16 + key % 16 : kk * 32 + key;
-        ka[kk] = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(kb + slot * 16 + 8 * half), 1.f);
+        ka[kk] = fp8x8_exact<DT>(*reinterpret_cast<const u32x2*>(kb + slot * 16 + 8 * half));
       }
       return;
     }
@@ -835,9 +835,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         const int g = kk / DT32;
         const int d = col + 32 * (kk % DT32);
         const int slot = TPP == 16 ? g * HD + d : d * 2 + g;
-        va[kk] = fp8x8_scaled<DT>(
-            *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half),
-            1.f);  // exact in 16 bits; the V scale is on P
+        // exact in 16 bits; the V scale is on P
+        va[kk] = fp8x8_exact<DT>(
+            *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half));
       } else {
         va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
       }
