@@ -105,11 +105,12 @@ struct Dt<kBF16> {
                                            acc, false);
   }
   // two fp8 e4m3 values (bytes 0-1, or 2-3 when hi) of w as a packed pair;
-  // exact: every e4m3 value is a bf16 value
+  // exact (every e4m3 value is a bf16 value): one v_cvt_scalef32_pk_bf16_fp8
+  // with scale 1
   static __device__ __forceinline__ uint32_t fp8x2(uint32_t w, bool hi) {
-    const f32x2 f = hi ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true)
-                       : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-    return pack2(f[0], f[1]);
+    const bf16x2 v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true)
+                        : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false);
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 
@@ -142,36 +143,22 @@ struct Dt<kF16> {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
   }
   // two fp8 e4m3 values as a packed pair; exact (e4m3's range and 3-bit
-  // mantissa fit fp16, subnormals included)
+  // mantissa fit fp16, subnormals included): one v_cvt_scalef32_pk_f16_fp8
+  // with scale 1
   static __device__ __forceinline__ uint32_t fp8x2(uint32_t w, bool hi) {
-    const f32x2 f = hi ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true)
-                       : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-    return pack2(f[0], f[1]);
+    const f16x2 v = hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, true)
+                       : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, false);
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 
 // Eight fp8 e4m3 values (w: bytes 0..7) as packed 16-bit values of dtype DT,
-// exactly (every e4m3 value, subnormals and NaN included, is a bf16 and an
-// fp16 value): one v_cvt_scalef32_pk_* per pair, with scale 1.
+// exactly (every finite e4m3 value, subnormals included, is a bf16 and an
+// fp16 value).
 template <int DT>
 __device__ __forceinline__ u32x4 fp8x8_exact(u32x2 w) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-  u32x4 r;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t word = q < 2 ? w.x : w.y;
-    if constexpr (DT == kBF16) {
-      const bf16x2_t v = (q & 1) ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.f, true)
-                                 : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.f, false);
-      r[q] = __builtin_bit_cast(uint32_t, v);
-    } else {
-      const f16x2_t v = (q & 1) ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.f, true)
-                                : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.f, false);
-      r[q] = __builtin_bit_cast(uint32_t, v);
-    }
-  }
-  return r;
+  return u32x4{Dt<DT>::fp8x2(w.x, false), Dt<DT>::fp8x2(w.x, true), Dt<DT>::fp8x2(w.y, false),
+               Dt<DT>::fp8x2(w.y, true)};
 }
 
 // Eight fp8 e4m3 values (w: bytes 0..7) times scale s, as packed 16-bit
