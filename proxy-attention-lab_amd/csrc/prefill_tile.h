@@ -14,13 +14,14 @@
 //    query tokens of one sequence times the (up to 16) query heads sharing a
 //    kv head, so one K/V tile in LDS serves the whole GQA group.
 //  * Per 32-key step the K and V tiles reach LDS by direct-to-LDS copies
-//    (global_load_lds_dwordx4, no registers), issued two steps ahead into four
+//    (global_load_lds_dwordx4, no registers), issued three steps ahead into four
 //    LDS buffers, with counted waits and one barrier per step.  Page ids come
 //    from an LDS copy of the tile's page-table slice.  Steps of dense prompt
 //    keys are copied the same way from the prompt rows (V rows untransposed,
-//    read back with transposing LDS reads).  Steps at the tile end, across
-//    the history / prompt boundary or in fp8 pools take a synchronous
-//    register path.
+//    read back with transposing LDS reads); fp8 pages in window mode as fp8
+//    bytes, converted in the operand reads.  Steps across the history /
+//    prompt boundary, with invalid page ids, or of fp8 pages in prompt mode
+//    take a synchronous register path.
 //  * Each wavefront computes S^T = K * Q^T with v_mfma_f32_32x32x16 (A = K
 //    from LDS, B = Q^T held in registers) and O^T += V^T * P^T with the same
 //    instruction.  In the transposed products a lane owns one M-row, so the
@@ -301,7 +302,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // item, no registers, nothing to wait for here.  Every wavefront issues exactly
   // 2*NL copies (items past the step go to a junk slot), so the wait counts
   // are the same on every wavefront.
-  // Slow step (invalid pages, history / prompt boundary, fp8): register loads,
+  // Slow step (invalid pages, history / prompt boundary, fp8 in prompt mode): register loads,
   // masked, then LDS stores -- synchronous, so it also drains the copies in
   // flight, which keeps the counted waits safe.
   // pg0 / pg1: the pages of the step's first and (TPP 16) second 16 keys.
