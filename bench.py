@@ -617,6 +617,15 @@ def run_extra(configs: set[str], dev, args) -> dict:
         rope_ms, _ = time_op(rope.run, steps, warm, stream)
         out["prefill"]["rope_fill"] = rope.report(rope_ms)
         del rope
+        # the same attention over fp8 e4m3 pools (per-(page, kv head) scales)
+        k8, ks = to_fp8_pages(to_fp8_k_layout(w.k_pool))
+        v8, vs = to_fp8_pages(w.v_pool)
+        f8_ms, _ = time_op(lambda: pal.paged_attention(w.queries, k8, v8, w.page_table, w.seq_lens, w.q2seq,
+                                                       w.q_offset, k_scales=ks, v_scales=vs), steps, warm, stream)
+        f8_tf = fl / (f8_ms * 1e-3) / 1e12
+        out["prefill"]["fp8_pages"] = {"attention_ms": round(f8_ms, 4), "TFLOP/s": round(f8_tf, 1),
+                                       "frac_of_mfma_bf16_peak": round(f8_tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del k8, v8, ks, vs
         del w
         torch.cuda.empty_cache()
         pw = PromptWorkload(dev)
