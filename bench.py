@@ -444,7 +444,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the operators shard by KV head or sequence with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the operators would shard by KV head or sequence with no exchange)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
