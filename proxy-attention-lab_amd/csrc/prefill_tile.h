@@ -853,6 +853,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         } else {
           pp[q] = Dt<DT>::pack2(pe[2 * q], pe[2 * q + 1]);
         }
+        // consumed here, so the exponentials and the conversion stay in this
+        // chunk beside its QK MFMA (the fences only bind the scheduler: code
+        // motion would otherwise sink them to the PV MFMAs that use them,
+        // past the copy branches)
+        asm volatile("" ::"v"(pp[q]));
       }
       sched_fence();
     }
