@@ -816,6 +816,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
     u32x4 va[KS];  // PV operand m: k-step m / DT32, row tile m % DT32 (KS == 2 * DT32)
+    u32x2 v8[F8 ? KS : 1];  // fp8: the raw bytes of each chunk's V operand
     uint32_t pp[8];  // packed probabilities of the lane's scores 2q, 2q+1
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
@@ -836,9 +837,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         const int g = kk / DT32;
         const int d = col + 32 * (kk % DT32);
         const int slot = TPP == 16 ? g * HD + d : d * 2 + g;
-        // exact in 16 bits; the V scale is on P
-        va[kk] = fp8x8_exact<DT>(
-            *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half));
+        // exact in 16 bits; the V scale is on P.  Chunk kk converts the
+        // operand read in chunk kk - 1 (its LDS read has landed by then) and
+        // consumes it there, so the conversions are not sunk to the PV MFMAs.
+        v8[kk] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half);
+        if (kk > 0) {
+          va[kk - 1] = fp8x8_exact<DT>(v8[kk - 1]);
+          asm volatile("" ::"v"(va[kk - 1]));
+        }
+        if (kk == KS - 1) va[kk] = fp8x8_exact<DT>(v8[kk]);
       } else {
         va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
       }
