@@ -84,24 +84,49 @@ class PagePool:
         return src, dst
 
     @staticmethod
-    def apply_moves(src: np.ndarray, dst: np.ndarray, k_pool: torch.Tensor, v_pool: torch.Tensor,
-                    page_tables=(), k_scales: torch.Tensor | None = None, v_scales: torch.Tensor | None = None,
-                    stream=None) -> None:
-        """Copy pages src[m] -> dst[m] of both pools (and fp8 scale rows) on
-        the GPU, then rewrite every page table in ``page_tables`` (uint32 /
-        int32 device tensors, updated in place) through the same map."""
-        from .ops import _on_stream, _stream_handle
-
-        device = k_pool.device
-        num_pages = int(k_pool.shape[0])
+    def _check_targets(k_pool: torch.Tensor, v_pool: torch.Tensor, page_tables, k_scales, v_scales) -> None:
+        """Everything a compaction writes, checked before anything is planned
+        or launched: a rejected call leaves the allocator, the pools and the
+        page tables as they were."""
         for name, t in (("k_pool", k_pool), ("v_pool", v_pool)):
-            if not t.is_contiguous() or t.device != device:
+            if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+                raise ValueError(f"[compact] {name} must be a tensor on a HIP device")
+        device = k_pool.device
+        for name, t in (("k_pool", k_pool), ("v_pool", v_pool)):
+            if not t.is_contiguous() or t.device != device or t.dim() < 2:
                 raise ValueError(f"[compact] {name} must be contiguous on {device}")
+        num_pages, hkv = int(k_pool.shape[0]), int(k_pool.shape[1])
         page_bytes = k_pool[0].numel() * k_pool.element_size()
         if v_pool[0].numel() * v_pool.element_size() != page_bytes or int(v_pool.shape[0]) != num_pages:
             raise ValueError("[compact] K and V pools must hold the same pages of the same size")
         if (k_scales is None) != (v_scales is None):
             raise ValueError("[compact] give both k_scales and v_scales, or neither")
+        for name, t in (("k_scales", k_scales), ("v_scales", v_scales)):
+            if t is not None and (not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or
+                                  tuple(t.shape) != (num_pages, hkv) or not t.is_contiguous() or t.device != device):
+                raise ValueError(f"[compact] {name} must be contiguous float32 [{num_pages}, {hkv}] on {device}")
+        for pt in page_tables:
+            # rewritten in place by the kernel, so only 32-bit tables qualify
+            # (an int64 table would need a copy the caller never sees)
+            if not isinstance(pt, torch.Tensor) or pt.dtype not in (torch.int32, torch.uint32) or \
+                    not pt.is_contiguous() or pt.device != device:
+                raise ValueError("[compact] page tables must be contiguous int32 / uint32 device tensors")
+
+    @staticmethod
+    def apply_moves(src: np.ndarray, dst: np.ndarray, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                    page_tables=(), k_scales: torch.Tensor | None = None, v_scales: torch.Tensor | None = None,
+                    stream=None) -> None:
+        """Copy pages src[m] -> dst[m] of both pools (and fp8 scale rows) on
+        the GPU, then rewrite every page table in ``page_tables`` (uint32 /
+        int32 device tensors, updated in place) through the same map.  Every
+        argument is checked before the first launch."""
+        from .ops import _on_stream, _stream_handle
+
+        page_tables = tuple(page_tables)
+        PagePool._check_targets(k_pool, v_pool, page_tables, k_scales, v_scales)
+        device = k_pool.device
+        num_pages = int(k_pool.shape[0])
+        page_bytes = k_pool[0].numel() * k_pool.element_size()
         src = np.ascontiguousarray(src, np.uint32)
         dst = np.ascontiguousarray(dst, np.uint32)
         if src.shape != dst.shape or len(np.intersect1d(src, dst)):
@@ -122,14 +147,19 @@ class PagePool:
                                         v_scales.data_ptr() if v_scales is not None else None,
                                         num_pages, hkv, page_bytes, s_d.data_ptr(), d_d.data_ptr(), int(src.size), sh))
             for pt in page_tables:
-                if pt.dtype not in (torch.int32, torch.uint32) or not pt.is_contiguous() or pt.device != device:
-                    raise ValueError("[compact] page tables must be contiguous int32 / uint32 device tensors")
                 _lib.check(L.pal_remap_pages(pt.data_ptr(), pt.numel(), r_d.data_ptr(), num_pages, sh))
 
     def compact(self, k_pool: torch.Tensor, v_pool: torch.Tensor, page_tables=(),
                 k_scales: torch.Tensor | None = None, v_scales: torch.Tensor | None = None, stream=None) -> int:
         """Compaction in one call: plan, move the pages, rewrite the page
-        tables.  Returns the number of pages moved."""
+        tables.  Returns the number of pages moved.  The pools, scales and
+        page tables are checked first (and the pools must hold this
+        allocator's ``num_pages``): a ValueError leaves the allocator and
+        every tensor unchanged."""
+        page_tables = tuple(page_tables)
+        self._check_targets(k_pool, v_pool, page_tables, k_scales, v_scales)
+        if int(k_pool.shape[0]) != self.num_pages:
+            raise ValueError(f"[compact] the pools hold {int(k_pool.shape[0])} pages, the allocator {self.num_pages}")
         src, dst = self.compaction_plan()
         self.apply_moves(src, dst, k_pool, v_pool, page_tables, k_scales, v_scales, stream)
         return int(src.size)

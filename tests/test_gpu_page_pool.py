@@ -89,3 +89,38 @@ def test_compaction_moves_pages_and_keeps_decode(kv):
     assert live.max() < pool.num_used  # the live pages are now [0, live)
     after = host_bits(pal.paged_attention_decode(q, kd, vd, ptd, lensd, **extra))
     assert np.array_equal(before, after), "decode changed across compaction"
+
+
+def test_rejected_compact_leaves_allocator_and_tables():
+    """An int64 page table, wrong-shaped scales or a pool of another size are
+    rejected before the plan is recorded or any page moves."""
+    num_pages, hkv, hd, tpp = 16, 2, 64, 16
+    pool = pal.PagePool(num_pages)
+    pool.allocate(10)
+    pool.free([0, 3, 4])
+    k = torch.arange(num_pages * hkv * hd * tpp, dtype=torch.float32, device=DEV).to(torch.bfloat16)
+    k = k.view(num_pages, hkv, hd // 8, tpp, 8)
+    v = k.clone().view(num_pages, hkv, hd, tpp)
+    k0, v0 = k.clone(), v.clone()
+    good = dev_index(np.array([[1, 2, 5, 6], [7, 8, 9, 0]], np.uint32), torch.uint32)
+    bad64 = good.view(torch.int32).to(torch.int64)
+    announce("page-pool compaction rejected before planning")
+    with pytest.raises(ValueError, match="page tables"):
+        pool.compact(k, v, [good, bad64])
+    with pytest.raises(ValueError, match="k_scales"):
+        pool.compact(k, v, [good], k_scales=torch.ones((num_pages, hkv + 1), device=DEV),
+                     v_scales=torch.ones((num_pages, hkv), device=DEV))
+    with pytest.raises(ValueError, match="pages"):
+        pool.compact(k[:8], v[:8], [good])
+    torch.cuda.synchronize()
+    assert pool.num_free == 9
+    assert torch.equal(k, k0) and torch.equal(v, v0)
+    assert good.view(torch.int32).tolist() == [[1, 2, 5, 6], [7, 8, 9, 0]]
+    assert bad64.tolist() == [[1, 2, 5, 6], [7, 8, 9, 0]]
+    # the accepted call then compacts as planned: live pages 1,2,5..9 -> [0, 7)
+    assert pool.compact(k, v, [good]) == 3
+    torch.cuda.synchronize()
+    src, dst = np.array([7, 8, 9], np.uint32), np.array([0, 3, 4], np.uint32)
+    assert np.array_equal(good.view(torch.int32).cpu().numpy().view(np.uint32),
+                          orc.remap_table(np.array([[1, 2, 5, 6], [7, 8, 9, 0]], np.uint32), src, dst, num_pages))
+    assert torch.equal(k[0], k0[7]) and torch.equal(v[4], v0[9])

@@ -82,3 +82,24 @@ def test_oracle_apply_and_remap():
     assert np.array_equal(out[0], pool[4]) and np.array_equal(out[2], pool[5]) and np.array_equal(out[1], pool[1])
     t = np.array([[4, 1, 5], [3, 9, 0]], np.uint32)
     assert orc.remap_table(t, src, dst, 6).tolist() == [[0, 1, 2], [3, 9, 0]]
+
+
+def test_rejected_compact_changes_nothing():
+    """compact() checks its pools and tables before it plans: a rejected call
+    leaves the allocator's state (and the caller's tables) as they were."""
+    import torch
+
+    pool = pal.PagePool(8)
+    pool.allocate(6)
+    pool.free([1, 2])
+    free_before = pool.num_free
+    k = torch.zeros((8, 1, 2, 16, 8), dtype=torch.bfloat16)  # host tensors: not a HIP device
+    v = torch.zeros((8, 1, 16, 16), dtype=torch.bfloat16)
+    table = torch.tensor([[0, 3, 4, 5]], dtype=torch.int64)
+    with pytest.raises(ValueError, match="HIP device"):
+        pool.compact(k, v, [table])
+    assert pool.num_free == free_before
+    assert table.tolist() == [[0, 3, 4, 5]]
+    # the plan is still the one the allocator held before the rejected call
+    src, dst = pool.compaction_plan()
+    assert src.tolist() == [4, 5] and dst.tolist() == [1, 2]
