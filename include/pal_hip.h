@@ -9,8 +9,12 @@
  *
  * Conventions
  *  - All tensor arguments are raw device pointers to contiguous row-major
- *    buffers allocated by the caller; the library never allocates or frees
- *    device memory.
+ *    buffers allocated by the caller; no entry point allocates or frees
+ *    device memory.  The one static reservation: a 64 MiB `__device__`
+ *    scratch array (the no-allocation decode entry's workspace) that the
+ *    code object holds on every GPU where the library is loaded, whether
+ *    or not that entry is called (the PAL_DEBUG_CHECKS build,
+ *    libpal_hip_debug.so, holds its own copy).
  *  - fp16 / bf16 data is passed as `void*`, with a dtype code.
  *  - `stream` is a hipStream_t passed as `void*` (NULL = the null stream).
  *    Launches are asynchronous; the caller synchronises.
@@ -102,7 +106,8 @@ int pal_fill_kv_pages(const void* new_keys, const void* new_values, void* k_pool
  * ([N, Hkv, HD], src_dtype f16, bf16 or f32) are quantized with the
  * caller's per-(page, kv head) scales (k_scales / v_scales, fp32
  * [num_pages, Hkv]): q = x / scale, held to [-448, 448], rounded to nearest
- * even.  head_dim % 16 == 0, head_dim <= 256.  In place.
+ * even.  head_dim 64, 128 or 256 (the head dims the fp8 attention entries
+ * read; others are rejected).  In place.
  */
 int pal_fill_kv_pages_fp8(const void* new_keys, const void* new_values, int src_dtype, void* k_pool, void* v_pool,
                           const float* k_scales, const float* v_scales, const uint32_t* page_table,

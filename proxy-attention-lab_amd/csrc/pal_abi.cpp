@@ -223,6 +223,11 @@ int fill_call(const char* op, const FillArgs& a, hipStream_t stream) {
   const int chunk_dims = fp8 ? 16 : 8;  // one K stripe
   if (a.head_dim % chunk_dims != 0)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] head_dim %d must be a multiple of %d", op, a.head_dim, chunk_dims);
+  // fp8 pools are written only at the head dims the fp8 attention kernels
+  // read (a pool no kernel can attend over would only fail later)
+  if (fp8 && a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256)
+    return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] fp8 pools: no attention kernel for head_dim %d (supported: 64, 128, "
+                "256)", op, a.head_dim);
   if (a.head_dim > pal::kMaxFillHeadDim)
     return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] head_dim %d above the supported %d", op, a.head_dim,
                 pal::kMaxFillHeadDim);

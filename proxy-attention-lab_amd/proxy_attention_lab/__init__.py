@@ -18,6 +18,7 @@ from proxy_attention_lab.ops import (
     paged_attention,
     paged_attention_decode,
     paged_attention_prefill,
+    release_workspaces,
     rope_cos_sin_cache,
     rope_fill_kv_pages,
 )
@@ -33,6 +34,7 @@ __all__ = [
     "paged_attention",
     "paged_attention_decode",
     "paged_attention_prefill",
+    "release_workspaces",
     "rope_cos_sin_cache",
     "rope_fill_kv_pages",
     "FP8_DTYPE",

@@ -19,6 +19,7 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
+import collections
 import contextlib
 
 import torch
@@ -40,6 +41,7 @@ __all__ = [
     "paged_attention",
     "paged_attention_decode",
     "paged_attention_prefill",
+    "release_workspaces",
 ]
 
 
@@ -98,21 +100,29 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-_WORKSPACES: dict[tuple[str, int, int], torch.Tensor] = {}
+_WORKSPACES: "collections.OrderedDict[tuple[str, int, int], torch.Tensor]" = collections.OrderedDict()
+_WORKSPACES_PER_DEVICE = 4  # streams whose workspaces are kept per (operator, device), most recent first
 
 
 def _workspace(kind: str, nbytes: int, device: torch.device, stream_handle: int) -> torch.Tensor | None:
-    """Persistent, zero-initialised workspace per (operator, device, stream).
+    """Zero-initialised workspace per (operator, device, stream), kept for the
+    streams used most recently.
 
     The decode kernels keep a work-claim counter in it that must read zero
     when a call starts; every call leaves it zero again, so the buffer is
     reused as is by the next call of the same operator on the same stream
     (calls on one stream never overlap).  A larger request replaces it with a
-    new zeroed buffer.
+    new zeroed buffer.  At most ``_WORKSPACES_PER_DEVICE`` streams keep one
+    per (operator, device); the least recently used is dropped beyond that.
+    Dropping is safe while kernels on that stream still read it: the
+    buffer was allocated on that stream, so torch's caching allocator
+    hands its memory out again only to later work of the same stream.
+    ``release_workspaces`` drops them all.
     """
     if nbytes <= 0:
         return None
-    key = (kind, device.index if device.index is not None else torch.cuda.current_device(), stream_handle)
+    dev_index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (kind, dev_index, stream_handle)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         # allocated and zero-filled on the launch stream (the caller holds
@@ -120,7 +130,25 @@ def _workspace(kind: str, nbytes: int, device: torch.device, stream_handle: int)
         # queued on that stream, is only reused after them
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
+    _WORKSPACES.move_to_end(key)
+    same = [k for k in _WORKSPACES if k[0] == kind and k[1] == dev_index]
+    for k in same[:-_WORKSPACES_PER_DEVICE]:
+        del _WORKSPACES[k]
     return ws
+
+
+def release_workspaces(device: torch.device | int | None = None) -> int:
+    """Drop the operators' cached workspaces (of one device, or all); returns
+    how many were dropped.  Their memory goes back to torch's caching
+    allocator (``torch.cuda.empty_cache`` returns it to the device).  The
+    next call on a stream allocates a fresh zeroed workspace."""
+    if device is not None:
+        device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+    idx = None if device is None else (device.index if device.index is not None else torch.cuda.current_device())
+    drop = [k for k in _WORKSPACES if idx is None or k[1] == idx]
+    for k in drop:
+        del _WORKSPACES[k]
+    return len(drop)
 
 
 def _pools(op: str, k_pool: torch.Tensor, v_pool: torch.Tensor, device: torch.device, dtype: torch.dtype):

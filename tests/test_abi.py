@@ -55,6 +55,11 @@ def test_fill_rejects_bad_arguments_without_launch():
     assert st == _lib.PAL_ERR_INVALID_ARGUMENT and "multiple of 8" in _lib.last_error()
     # zero tokens is a no-op
     assert lib.pal_fill_kv_pages(None, None, None, None, None, None, None, 1, 0, 2, 64, 16, 8, 1, 1, None) == 0
+    # fp8 pools only at head dims an fp8 attention kernel reads (64, 128, 256)
+    for hd in (16, 48, 80, 96, 192):
+        st = lib.pal_fill_kv_pages_fp8(None, None, 1, None, None, None, None, None, None, None, 4, 2, hd, 16, 8, 1, 1,
+                                       None)
+        assert st == _lib.PAL_ERR_INVALID_ARGUMENT and "no attention kernel" in _lib.last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.PAL_ERR_INVALID_ARGUMENT)
 

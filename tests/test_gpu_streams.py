@@ -100,3 +100,33 @@ def test_prefill_on_side_stream_int64_strided():
     torch.cuda.synchronize()
     ref = orc.paged_attention_prefill(q, k, v, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "bf16")
     assert_close(host_f32(out), ref, "bf16", "prefill side stream")
+
+
+def test_workspace_cache_is_bounded_and_releasable():
+    """Calls on many streams keep workspaces for the most recent few only,
+    results stay right on every stream, and release_workspaces drops them."""
+    from proxy_attention_lab import ops as pal_ops
+
+    case = make_paged_case(81, [700, 33, 2500], 8, 2, 64, 16, "f16")
+    q = randn_bits(np.random.default_rng(81), (3, 8, 64), "f16")
+    qd, kd, vd = dev_bits(q, "f16"), dev_bits(case.k_pool, "f16"), dev_bits(case.v_pool, "f16")
+    pt, lens = _i64(case.page_table), _i64(case.seq_lens)
+    ref = orc.paged_attention_decode(q, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "f16")
+    announce("decode on 7 streams: bounded workspace cache")
+    pal.release_workspaces()
+    streams = [torch.cuda.Stream() for _ in range(7)]
+    outs = []
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+        outs.append(pal.paged_attention_decode(qd, kd, vd, pt, lens, stream=s))
+    torch.cuda.synchronize()
+    kept = [k for k in pal_ops._WORKSPACES if k[0] == "decode"]
+    assert len(kept) == pal_ops._WORKSPACES_PER_DEVICE
+    assert {k[2] for k in kept} == {s.cuda_stream for s in streams[-pal_ops._WORKSPACES_PER_DEVICE:]}
+    for o in outs:
+        assert_close(host_f32(o), ref, "f16", "decode on a side stream (bounded cache)")
+    assert pal.release_workspaces() >= len(kept)
+    assert not pal_ops._WORKSPACES
+    out = pal.paged_attention_decode(qd, kd, vd, pt, lens)
+    torch.cuda.synchronize()
+    assert_close(host_f32(out), ref, "f16", "decode after release_workspaces")
