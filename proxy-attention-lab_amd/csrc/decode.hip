@@ -1016,48 +1016,47 @@ void fused_kernel(const DecodeParams dp, const PrefillParams pp, const unsigned 
 //
 // The worker that wrote slot v holds the segment's first piece, so the
 // contributors are v, v+1, ...: the list slot, the header and the partials of
-// the first kSpec contributors (both partial slots of v, whose piece may be
-// its first or its last, and the first-piece slot of the others) are all
-// fetched in one round trip, before the slot says how many there are.  A
-// segment with more contributors is finished by the general loop: lane j
-// fetches the (m, l) of the j-th contributor and the O loads of consecutive
-// contributors are unrolled.  Workgroup 0 re-arms the claim counter.
+// the first contributors are all fetched in one round trip, before the slot
+// says how many there are.  A wavefront fetches one head's four candidate
+// rows at once -- both partial slots of v (its piece may be v's first or its
+// last) and the first-piece slots of v+1 and v+2 -- one row per 16 lanes,
+// 8 dims (16 bytes) per lane, plus each row's (max, exp-sum): two load
+// instructions per head instead of one per element.  A segment with more
+// than three contributors is finished by the general loop.  Workgroup 0
+// re-arms the claim counter.
 template <int DT, int HD, int TPP>
 __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const DecodeParams p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
   const int lane = lane_id();
   const int wv = wave_id();
-  constexpr int kPer = (HD + kWave - 1) / kWave;
-  constexpr int kSpec = 3;                              // contributors fetched with the slot
-  constexpr int kBatch = 8;                             // general path: O loads in flight
+  constexpr int kCh = (HD + 127) / 128;                 // 8-dim chunks of a row per lane (16 lanes per row)
   constexpr int kHpw = 16 / kWorkersPerGroup;           // heads per wavefront (hg_max <= 16)
+  constexpr int kBatch = 8;                             // general path: O loads in flight
   const int64_t last_w = p.list_cap - 1;                // partial slots exist for workers < list_cap
+  const int cand = lane >> 4;                           // candidate row: 0, 1 = slots of e; 2, 3 = slot 0 of e+1, e+2
+  const int rl16 = lane & 15;
 
   int64_t sg0 = 0, snb = 0, srow = 0, sseg = 0;
-  float pm[kHpw][kSpec + 1], pl[kHpw][kSpec + 1], po[kHpw][kSpec + 1][kPer];
-  // index t: 0 = slot 0 of worker e, 1 = slot 1 of worker e, t >= 2 = slot 0 of worker e + t - 1
+  f32x2 pml[kHpw];
+  u32x4 po[kHpw][kCh];
   auto fetch = [&](int64_t e) {
     const int64_t* slot = p.split_list + 4 * e;
     sg0 = slot[0];
     snb = slot[1];
     srow = slot[2];
     sseg = slot[3];
+    int64_t u = cand < 2 ? e : e + cand - 1;
+    u = u < last_w ? u : last_w;
 #pragma unroll
     for (int j = 0; j < kHpw; ++j) {
       const int h = wv + kWorkersPerGroup * j;
       if (h < p.hg_max) {
+        const int64_t sl = (u * 2 + (cand == 1 ? 1 : 0)) * p.hg_max + h;
+        pml[j] = *reinterpret_cast<const f32x2*>(p.part_ml + sl * 2);
 #pragma unroll
-        for (int t = 0; t <= kSpec; ++t) {
-          int64_t u = t < 2 ? e : e + t - 1;
-          u = u < last_w ? u : last_w;
-          const int64_t sl = (u * 2 + (t == 1 ? 1 : 0)) * p.hg_max + h;
-          pm[j][t] = p.part_ml[sl * 2];
-          pl[j][t] = p.part_ml[sl * 2 + 1];
-#pragma unroll
-          for (int q = 0; q < kPer; ++q) {
-            const int d = lane + q * kWave;
-            po[j][t][q] = d < HD ? Dt<DT>::to_f32(p.part_o[sl * HD + d]) : 0.f;
-          }
+        for (int c = 0; c < kCh; ++c) {
+          const int d = 8 * rl16 + 128 * c;
+          po[j][c] = d < HD ? *reinterpret_cast<const u32x4*>(p.part_o + sl * HD + d) : u32x4{0u, 0u, 0u, 0u};
         }
       }
     }
@@ -1081,40 +1080,46 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
       const int64_t v0 = vworker_of(sc, g0);
       const int64_t v1 = vworker_of(sc, g0 + nb - 1);
       const int64_t nc = v1 - v0 + 1;
-      if (v0 == e && nc <= kSpec) {
-        // the common case: everything is in registers already
+      if (v0 == e && nc <= 3) {
+        // the common case: every contributor's row is in registers already.
+        // Contributor 0 is candidate t0 (slot 0 of e if the segment starts
+        // e's range, else slot 1), contributors 1 and 2 candidates 2 and 3.
         const int t0 = vstart(sc, e) >= g0 ? 0 : 1;
+        const bool live = cand == t0 || (cand >= 2 && cand - 1 < nc);
 #pragma unroll
         for (int j = 0; j < kHpw; ++j) {
           const int h = wv + kWorkersPerGroup * j;
           if (h >= hg) continue;
-          float big_m = -INFINITY;
-#pragma unroll
-          for (int t = 1; t <= kSpec; ++t) {
-            const int k = t == 1 ? t0 : t;  // contributor t-1
-            if (t - 1 < nc) big_m = fmaxf(big_m, pm[j][k]);
-          }
+          const float m = live ? pml[j].x : -INFINITY;
+          float big_m = fmaxf(m, shfl_xor(m, 16));
+          big_m = fmaxf(big_m, shfl_xor(big_m, 32));
           const float base_m = (big_m == -INFINITY) ? 0.f : big_m;
-          float lsum = 0.f;
-          float acc[kPer];
-#pragma unroll
-          for (int q = 0; q < kPer; ++q) acc[q] = 0.f;
-#pragma unroll
-          for (int t = 1; t <= kSpec; ++t) {
-            const int k = t == 1 ? t0 : t;
-            if (t - 1 < nc) {
-              const float w = __builtin_amdgcn_exp2f(pm[j][k] - base_m) * pl[j][k];
-              lsum += w;
-#pragma unroll
-              for (int q = 0; q < kPer; ++q) acc[q] += w * po[j][k][q];
-            }
-          }
+          // dead candidates may hold anything (an earlier call's rows, or
+          // never-written bytes): their weight and products are zero by select
+          float w = live ? __builtin_amdgcn_exp2f(m - base_m) * pml[j].y : 0.f;
+          float lsum = w + shfl_xor(w, 16);
+          lsum += shfl_xor(lsum, 32);
           const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
           const int64_t row = out_row * p.num_q_heads + kvh * p.group + h0 + h;  // output row
 #pragma unroll
-          for (int q = 0; q < kPer; ++q) {
-            const int d = lane + q * kWave;
-            if (d < HD) p.out[row * HD + d] = Dt<DT>::from_f32(acc[q] * inv);
+          for (int c = 0; c < kCh; ++c) {
+            const int d = 8 * rl16 + 128 * c;
+            float acc[8];
+#pragma unroll
+            for (int e8 = 0; e8 < 8; ++e8) {
+              const uint32_t word = po[j][c][e8 >> 1];
+              const float y = Dt<DT>::to_f32(static_cast<uint16_t>((e8 & 1) ? (word >> 16) : (word & 0xFFFFu)));
+              acc[e8] = live ? w * y : 0.f;
+              acc[e8] += shfl_xor(acc[e8], 16);
+              acc[e8] += shfl_xor(acc[e8], 32);
+            }
+            if (cand == 0 && d < HD) {  // out is 8-byte aligned: two 8-byte stores
+              uint16_t* dst = p.out + row * HD + d;
+              const u32x2 lo = {Dt<DT>::pack2(acc[0] * inv, acc[1] * inv), Dt<DT>::pack2(acc[2] * inv, acc[3] * inv)};
+              const u32x2 hi = {Dt<DT>::pack2(acc[4] * inv, acc[5] * inv), Dt<DT>::pack2(acc[6] * inv, acc[7] * inv)};
+              *reinterpret_cast<u32x2*>(dst) = lo;
+              *reinterpret_cast<u32x2*>(dst + 4) = hi;
+            }
           }
         }
       } else {
@@ -1153,10 +1158,10 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
               const int64_t j = c0 + static_cast<int64_t>(u) * kRpi + rg;
-              const bool live = j < nc;
-              const int64_t sl = slot_j(live ? j : nc - 1, h);  // padding re-reads the last row
+              const bool jl = j < nc;
+              const int64_t sl = slot_j(jl ? j : nc - 1, h);  // padding re-reads the last row
               mb[u] = p.part_ml[sl * 2];
-              lb[u] = live ? p.part_ml[sl * 2 + 1] : 0.f;
+              lb[u] = jl ? p.part_ml[sl * 2 + 1] : 0.f;
               ob[u] = dl ? *reinterpret_cast<const u32x4*>(p.part_o + sl * HD + rl * 8) : u32x4{0u, 0u, 0u, 0u};
             }
 #pragma unroll
@@ -1194,13 +1199,169 @@ __global__ __launch_bounds__(kGroupThreads) void decode_merge_kernel(const Decod
   }
 }
 
-// The merge of split segments, after the stream kernel.  Live merge slots:
-// one per static share (at most num_workers) with equal shares, up to
-// list_cap in the fixed-chunk mode.  A workgroup with no live slot still pays
-// one fetch round trip, so the equal-share grid is not padded beyond the
-// workers (it then fits the GPU in one round).
+// The merge for batches with few segments per worker (plain decode in the
+// fixed-chunk mode, or with fewer segments than a quarter of the resident
+// workers -- long contexts, where one segment has tens to thousands of
+// contributors).  Instead of walking the merge list one workgroup per slot
+// (a chain of round trips per segment), the grid enumerates the merge's
+// outputs: workgroup b is unit (item s, segment k, head h, slice of
+// kSegDims dims).  It finds the segment's blocks from the length scan
+// (cum[s] + k nb .. + nb), hence its contributors v0 .. v1 by the fixed cut;
+// its 256 threads are 64 contributor lanes x 4 groups of 8 dims, each lane
+// loading (max, exp-sum) and 16 bytes of O of a batch of kBatch
+// contributors per round trip (512 contributors per round trip per
+// workgroup).  Each thread keeps a running max (rescaling its sums when it
+// grows), and the lanes' sums are combined by the same log-sum-exp rule,
+// across lanes with shuffles and across the wavefronts through LDS.
+constexpr int kSegDims = 32;
+
+template <int DT, int HD, int TPP>
+__global__ __launch_bounds__(kGroupThreads) void decode_merge_seg_kernel(const DecodeParams p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.claim = 0u;
+  constexpr int kDs = HD < kSegDims ? HD : kSegDims;
+  constexpr int kSlices = (HD + kDs - 1) / kDs;
+  constexpr int kDg = kDs / 8;                 // 8-dim groups per slice
+  constexpr int kCl = kGroupThreads / kDg;     // contributor lanes of the workgroup
+  constexpr int kClw = kWave / kDg;            // of one wavefront
+  constexpr int kBatch = 8;
+  static_assert(kDs % 8 == 0, "slices of whole 8-dim groups");
+  __shared__ float red[kWorkersPerGroup][kDg][10];
+  const int tid = threadIdx.x;
+  const int dg = tid % kDg;
+  const int cl = tid / kDg;
+  int64_t u = blockIdx.x;
+  const int slice = static_cast<int>(u % kSlices);
+  u /= kSlices;
+  const int h = static_cast<int>(u % p.hg_max);
+  u /= p.hg_max;
+  const int segs = p.num_kv_heads * p.head_chunks;
+  const int k = static_cast<int>(u % segs);
+  const int64_t s = u / segs;
+  const int kvh = k / p.head_chunks;
+  const int h0 = (k % p.head_chunks) * 16;
+  const int hg = min(16, p.group - h0);
+  // every return below is uniform over the workgroup (before its barrier)
+  if (s >= p.num_seqs || h >= hg) return;
+  const Item it = item_at(p, s, TPP);
+  const int64_t nb = (it.len + 15) >> 4;
+  if (nb == 0) return;
+  const int64_t total = p.hdr[0];  // > 0: this item has blocks
+  const Sched sc = make_sched(total, p.num_workers, p.tokens_per_worker);
+  const int64_t g0 = p.cum[s] + static_cast<int64_t>(k) * nb;
+  const int64_t v0 = vworker_of(sc, g0);
+  const int64_t nc = vworker_of(sc, g0 + nb - 1) - v0 + 1;
+  if (nc <= 1) return;  // a whole segment: its worker wrote the output
+  const int t0 = vstart(sc, v0) >= g0 ? 0 : 1;  // contributor 0's partial slot
+  const int d = slice * kDs + dg * 8;
+  const bool dl = d < HD;
+
+  float m_loc = -INFINITY, l_loc = 0.f;
+  float acc[8];
+#pragma unroll
+  for (int e8 = 0; e8 < 8; ++e8) acc[e8] = 0.f;
+  for (int64_t c0 = 0; c0 < nc; c0 += static_cast<int64_t>(kCl) * kBatch) {
+    f32x2 mlb[kBatch];
+    u32x4 ob[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int64_t j = c0 + static_cast<int64_t>(b) * kCl + cl;
+      const int64_t jj = j < nc ? j : nc - 1;  // padding re-reads the last row, with weight 0
+      const int64_t sl = ((v0 + jj) * 2 + (jj == 0 ? t0 : 0)) * p.hg_max + h;
+      mlb[b] = *reinterpret_cast<const f32x2*>(p.part_ml + sl * 2);
+      if (j >= nc) mlb[b] = f32x2{-INFINITY, 0.f};
+      ob[b] = dl ? *reinterpret_cast<const u32x4*>(p.part_o + sl * HD + d) : u32x4{0u, 0u, 0u, 0u};
+    }
+    float bm = m_loc;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) bm = fmaxf(bm, mlb[b].x);
+    if (bm > m_loc) {  // the running max grew: rescale this lane's sums
+      const float a = m_loc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_loc - bm);
+      l_loc *= a;
+#pragma unroll
+      for (int e8 = 0; e8 < 8; ++e8) acc[e8] *= a;
+      m_loc = bm;
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const float w = mlb[b].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mlb[b].x - m_loc) * mlb[b].y;
+      l_loc += w;
+#pragma unroll
+      for (int e8 = 0; e8 < 8; ++e8) {
+        const uint32_t word = ob[b][e8 >> 1];
+        acc[e8] += w * Dt<DT>::to_f32(static_cast<uint16_t>((e8 & 1) ? (word >> 16) : (word & 0xFFFFu)));
+      }
+    }
+  }
+  // (m, l, acc) of two lanes -> their log-sum-exp combination
+  auto combine = [&](float m2, float l2, const float (&a2)[8]) {
+    const float mm = fmaxf(m_loc, m2);
+    const float f1 = m_loc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_loc - mm);
+    const float f2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - mm);
+    l_loc = f1 * l_loc + f2 * l2;
+#pragma unroll
+    for (int e8 = 0; e8 < 8; ++e8) acc[e8] = f1 * acc[e8] + f2 * a2[e8];
+    m_loc = mm;
+  };
+  // across the contributor lanes of a wavefront (lane = cl_w * kDg + dg)
+#pragma unroll
+  for (int off = kDg; off < kWave; off <<= 1) {
+    const float m2 = shfl_xor(m_loc, off);
+    const float l2 = shfl_xor(l_loc, off);
+    float a2[8];
+#pragma unroll
+    for (int e8 = 0; e8 < 8; ++e8) a2[e8] = shfl_xor(acc[e8], off);
+    combine(m2, l2, a2);
+  }
+  const int wv = wave_id();
+  const int lane = lane_id();
+  if (lane < kDg) {
+    red[wv][dg][0] = m_loc;
+    red[wv][dg][1] = l_loc;
+#pragma unroll
+    for (int e8 = 0; e8 < 8; ++e8) red[wv][dg][2 + e8] = acc[e8];
+  }
+  __syncthreads();
+  if (wv != 0 || lane >= kDg) return;
+#pragma unroll
+  for (int w2 = 1; w2 < kWorkersPerGroup; ++w2) {
+    float a2[8];
+#pragma unroll
+    for (int e8 = 0; e8 < 8; ++e8) a2[e8] = red[w2][dg][2 + e8];
+    combine(red[w2][dg][0], red[w2][dg][1], a2);
+  }
+  static_assert(kClw >= 1, "a wavefront holds whole 8-dim groups");
+  if (!dl) return;
+  const float inv = l_loc > 0.f ? 1.f / l_loc : 0.f;
+  const int64_t row = it.row * p.num_q_heads + kvh * p.group + h0 + h;
+  uint16_t* dst = p.out + row * HD + d;  // out is 8-byte aligned: two 8-byte stores
+  const u32x2 lo = {Dt<DT>::pack2(acc[0] * inv, acc[1] * inv), Dt<DT>::pack2(acc[2] * inv, acc[3] * inv)};
+  const u32x2 hi = {Dt<DT>::pack2(acc[4] * inv, acc[5] * inv), Dt<DT>::pack2(acc[6] * inv, acc[7] * inv)};
+  *reinterpret_cast<u32x2*>(dst) = lo;
+  *reinterpret_cast<u32x2*>(dst + 4) = hi;
+}
+
+// The merge of split segments, after the stream kernel.  Plain decode with
+// few segments per worker (the fixed-chunk mode, or fewer segments than a
+// quarter of the resident workers): the segment-enumerating merge, one
+// workgroup per (item, segment, head, dim slice).  Otherwise the merge list:
+// one slot per static share (at most num_workers) with equal shares, up to
+// list_cap in the fixed-chunk mode.  A workgroup with no live slot still
+// pays one fetch round trip, so the equal-share grid is not padded beyond
+// the workers (it then fits the GPU in one round).
+constexpr int64_t kMaxSegMergeGroups = 1 << 16;
+
 template <int DT, int HD, int TPP>
 hipError_t launch_merge(const DecodeParams& p, hipStream_t stream) {
+  if (!p.q2seq) {
+    const int64_t segments = p.num_seqs * p.num_kv_heads * p.head_chunks;
+    constexpr int64_t slices = (HD + kSegDims - 1) / (HD < kSegDims ? HD : kSegDims);
+    const int64_t units = segments * p.hg_max * slices;
+    if ((p.tokens_per_worker > 0 || segments * 4 <= p.num_workers) && units > 0 && units <= kMaxSegMergeGroups) {
+      hipLaunchKernelGGL((decode_merge_seg_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(units)),
+                         dim3(kGroupThreads), 0, stream, p);
+      return hipGetLastError();
+    }
+  }
   int64_t merge_groups = p.tokens_per_worker == 0 ? p.num_workers : kMergeGroups;
   if (merge_groups > p.list_cap) merge_groups = p.list_cap;
   hipLaunchKernelGGL((decode_merge_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(merge_groups)),

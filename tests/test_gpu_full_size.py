@@ -170,3 +170,27 @@ def test_reference_signature_full_size():
     for i, s in enumerate(seqs):
         got = out_h[s * P * hq:(s + 1) * P * hq]
         assert_close(got, ref[i * P * hq:(i + 1) * P * hq], "bf16", f"reference signature seq {s} (history {int(w.hist[s])})")
+
+
+@pytest.mark.parametrize("partition", [512, 0])
+def test_long_history_decode_524288(partition):
+    """Batch-1 decode over a 524,288-token history, the top of the range the
+    reference times (benchmarks/paged_attention/cpp/seq_len_vs_latency.cpp:
+    210-223), at HD 128 bf16 with 4 query heads on 2 kv heads (the
+    reference benchmark's 2:1 grouping, fewer heads so the oracle's fp32 copy
+    of the pools fits host memory), 1 % of key rows x8.  Each segment is
+    shared by hundreds (equal shares) or a thousand (partition 512)
+    contributors, which the merge must combine."""
+    announce(f"long-history decode 524288 tokens partition {partition}: build")
+    w = bench.DecodeWorkload(21, num_seqs=1, ctx_lo=524288, ctx_hi=524288, hq=4, hkv=2, device=DEV)
+    rng = np.random.default_rng(21)
+    pos = rng.choice(524288, size=5242, replace=False)
+    pi = torch.from_numpy(w.pt_np[0, pos // w.tpp].astype(np.int64)).to(DEV)
+    si = torch.from_numpy((pos % w.tpp).astype(np.int64)).to(DEV)
+    w.k_pool[pi, :, :, si, :] = w.k_pool[pi, :, :, si, :] * 8
+    announce(f"long-history decode 524288 tokens partition {partition}: decode")
+    out_h = host_f32(w.decode(partition))
+    assert np.isfinite(out_h).all()
+    ref = orc.paged_attention_decode(host_bits(w.queries), host_bits(w.k_pool), host_bits(w.v_pool),
+                                     w.pt_np.astype(np.uint32), w.lens_np, "bf16")
+    assert_close(out_h, ref, "bf16", f"long-history decode 524288 tokens, 4/2 heads, partition {partition}")
