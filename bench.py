@@ -20,10 +20,13 @@ The other configs are reported beside it, each in its own object:
       over causal-valid pairs only
   c5  fused mixed batch, fp16: 256 decode rows + 4 prefill chunks of 1024
       rows, interleaved in shuffled row blocks, one operator call
-The CPU baseline is the numpy oracle on the host cores on a bounded sample
-of config 2.
+  lh  batch-1 decode over 131,072 / 524,288 / 1,048,576-token histories
+      (the reference benchmark's range), 32/16 heads, HD 128, bf16
+The CPU baseline is the reference's equivalency computation (gather pages +
+fp32 softmax attention) on torch CPU over the host cores: configs 1 and 2 in
+full, configs 3-5 on a stated subsample scaled by its share of the work.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5,lh]
 """
 
 from __future__ import annotations
@@ -363,61 +366,118 @@ class RopeFill:
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the numpy oracle on a bounded sample of the same workload
+# CPU baseline: the reference's equivalency computation (gather pages + fp32
+# softmax attention) on torch CPU, over the same inputs as the GPU run
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline(w: DecodeWorkload, budget_s: float = 12.0) -> dict:
+def _host_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_subset(k_pool: torch.Tensor, v_pool: torch.Tensor, pt: np.ndarray, lens: np.ndarray, seqs,
+                tpp: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Host bits of the pages sequences `seqs` use (their first lens[s]
+    tokens) and their page table renumbered to that compacted pool."""
+    used = []
+    for s in seqs:
+        used.extend(int(x) for x in pt[s, : (int(lens[s]) + tpp - 1) // tpp])
+    uniq = np.unique(np.asarray(used, np.int64)) if used else np.zeros(1, np.int64)
+    idx = torch.from_numpy(uniq).to(k_pool.device)
+    kb, vb = _host_bits(k_pool.index_select(0, idx)), _host_bits(v_pool.index_select(0, idx))
+    pos = {int(p): i for i, p in enumerate(uniq)}
+    spt = np.zeros((len(seqs), max(1, max((int(lens[s]) + tpp - 1) // tpp for s in seqs))), np.uint32)
+    for i, s in enumerate(seqs):
+        for j in range((int(lens[s]) + tpp - 1) // tpp):
+            spt[i, j] = pos[int(pt[s, j])]
+    return kb, vb, spt
+
+
+def config1_host() -> dict:
+    """Config 1: 4 sequences, ctx {64, 100, 192, 256},
+    Hq 4 / Hkv 1, HD 64, TPP 16, a 64-page pool assigned by a seeded random
+    permutation, N(0,1) fp16 values."""
+    rng = np.random.default_rng(100)
+    lens = np.array([64, 100, 192, 256], np.int32)
+    perm = rng.permutation(64)
+    pt = np.zeros((4, 16), np.uint32)
+    cur = 0
+    for s, n in enumerate(lens):
+        k = (int(n) + 15) // 16
+        pt[s, :k] = perm[cur:cur + k]
+        cur += k
+
+    def bits(shape):
+        return rng.standard_normal(shape).astype(np.float16).view(np.uint16)
+
+    return {"q": bits((4, 4, 64)), "k": bits((64, 1, 8, 16, 8)), "v": bits((64, 1, 64, 16)), "pt": pt,
+            "lens": lens, "dtype": "f16"}
+
+
+def _cpu_time(fn, reps: int, warm: int) -> float:
+    """Median wall seconds of `reps` calls after `warm` warm-up calls."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baseline(samples: dict) -> dict:
+    """The CPU restatement of PAL's equivalency path (the reference has no CPU
+    kernels, paged_attention_decode_primitive.cpp:63-69, and MLX is not
+    available offline) timed on the host cores: config 1 and config 2 in
+    full, configs 3-5 on a stated subsample scaled to the whole workload by
+    its share of the work.  torch CPU with one thread per core of the
+    process's affinity; median of several calls after warm-up."""
     from oracle import pal_oracle as orc  # the checker, used here only as the timed CPU baseline
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     cpu_model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
             cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), cpu_model)
     except OSError:  # pragma: no cover
         pass
-    dt = "bf16"
-    q = w.queries.view(torch.int16).cpu().numpy().view(np.uint16)
-    kb = w.k_pool.view(torch.int16).cpu().numpy().view(np.uint16)
-    vb = w.v_pool.view(torch.int16).cpu().numpy().view(np.uint16)
-    # sample: the first 8 sequences (their pages only), repeated until the time budget is used
-    ns = 8
-    lens = w.lens_np[:ns]
-    used = np.concatenate([w.pt_np[s, : (int(n) + w.tpp - 1) // w.tpp] for s, n in enumerate(lens)])
-    kb, vb = kb[used], vb[used]
-    pt = np.zeros((ns, w.pt_np.shape[1]), np.int32)
-    cur = 0
-    for s, n in enumerate(lens):
-        npg = (int(n) + w.tpp - 1) // w.tpp
-        pt[s, :npg] = np.arange(cur, cur + npg)
-        cur += npg
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        orc.paged_attention_decode(q[:ns], kb, vb, pt, lens, dt)
-        reps += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    el = (time.perf_counter() - t0) / reps
-    kv_bytes = int(lens.astype(np.int64).sum()) * 2 * w.hkv * w.hd * 2 + 2 * ns * w.hq * w.hd * 2
-    return {
-        "value": round(kv_bytes / el / 1e9, 3),
-        "unit": "GB/s",
-        "tokens_per_s": round(ns / el, 2),
-        "cores": int(cores),
-        "cpu_model": cpu_model,
-        "affinity_cpus": len(os.sched_getaffinity(0)),
-        "kind": "port",
-        "sample": f"numpy oracle (bf16->fp32 decode of the sample's pages, gather, fp32 softmax attention) on "
-                  f"{ns} of the 64 config-2 sequences ({int(lens.sum())} context tokens), {reps} reps in "
-                  f"{el * reps:.1f} s; fill step not included",
-    }
+    t_start = time.perf_counter()
+    res = {"unit": "GB/s", "cores": int(torch.get_num_threads()), "cpu_model": cpu_model,
+           "affinity_cpus": cores, "kind": "port"}
+
+    def run(sm, reps, warm):
+        return _cpu_time(lambda: orc.torch_cpu_paged_attention(sm["q"], sm["k"], sm["v"], sm["pt"], sm["lens"],
+                                                               sm["dtype"], sm.get("q2s"), sm.get("off")),
+                         reps, warm)
+
+    c1 = config1_host()
+    t1 = run(c1, 20, 3)
+    res["config1"] = {"ms": round(t1 * 1e3, 3), "sample": "config 1 in full (4 sequences)"}
+    c2 = samples["c2"]
+    t2 = run(c2, 10, 3)
+    res["value"] = round(c2["bytes"] / t2 / 1e9, 3)
+    res["tokens_per_s"] = round(len(c2["lens"]) / t2, 2)
+    res["config2_ms"] = round(t2 * 1e3, 2)
+    res["sample"] = (f"config 2 in full (64 sequences, {int(c2['lens'].sum())} context tokens, the same pools as "
+                     f"the GPU run's first copy): decode by gather + torch fp32 scaled_dot_product_attention, "
+                     f"median of 10 after 3 warm-up; the fill step not included")
+    for key, name in (("c3", "config3"), ("c4", "config4"), ("c5d", "config5_decode_rows"),
+                      ("c5p", "config5_prefill_rows")):
+        sm = samples.get(key)
+        if sm is None:
+            continue
+        t = run(sm, 3, 1)
+        rec = {"sample": sm["what"], "ms_sample": round(t * 1e3, 2), "scale": round(sm["scale"], 3),
+               "ms_scaled": round(t * sm["scale"] * 1e3, 1)}
+        if "bytes" in sm:
+            rec["GB/s"] = round(sm["bytes"] / (t * sm["scale"]) / 1e9, 3)
+        if "flops" in sm:
+            rec["TFLOP/s"] = round(sm["flops"] / (t * sm["scale"]) / 1e12, 4)
+        res[name] = rec
+    res["cpu_seconds"] = round(time.perf_counter() - t_start, 1)
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -433,9 +493,9 @@ def main() -> int:
     ap.add_argument("--rotate", type=int, default=4, help="independent workload copies cycled per step")
     ap.add_argument("--partition", type=int, default=0, help="decode partition size (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--configs", default="c2,c3,c4,c5",
-                    help="comma list of workloads to run (c2 is the headline; c3/c4/c5 are reported beside it)")
+    ap.add_argument("--configs", default="c2,c3,c4,c5,lh",
+                    help="comma list of workloads to run (c2 is the headline; c3/c4/c5 and lh, the long-history "
+                         "decode points, are reported beside it)")
     ap.add_argument("--extra-steps", type=int, default=20, help="timed calls per extra config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the timed loop, run one device-to-device copy of this many MiB (a kernel of "
@@ -460,8 +520,9 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     configs = {c.strip() for c in args.configs.split(",") if c.strip()}
+    samples: dict = {}  # host copies of the CPU baseline's inputs, taken from the GPU run's workloads
     if "c2" not in configs:
-        extra = run_extra(configs, dev, args)
+        extra = run_extra(configs, dev, args, samples)
         print(json.dumps({"metric": METRIC, "configs": sorted(configs), **extra}), flush=True)
         return 0
     works = [DecodeWorkload(seed=i) for i in range(max(1, args.rotate))]
@@ -565,17 +626,57 @@ def main() -> int:
         "tokens_per_s": round(w0.num_seqs / (f8_step_ms * 1e-3), 1),
     }
     result["rope_fill_config2"] = rope.report(rope_ms)
-    del works, rope
-    torch.cuda.empty_cache()
-    result.update(run_extra(configs, dev, args))
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w0, args.cpu_budget)
+        samples["c2"] = {"q": _host_bits(w0.queries), "k": _host_bits(w0.k_pool), "v": _host_bits(w0.v_pool),
+                         "pt": w0.pt_np.astype(np.uint32), "lens": w0.lens_np, "dtype": "bf16",
+                         "bytes": w0.decode_bytes()}
+    del works, rope, w0
+    torch.cuda.empty_cache()
+    result.update(run_extra(configs, dev, args, samples if not args.no_cpu_baseline else None))
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(samples)
     print(json.dumps(result), flush=True)
     return 0
 
 
-def run_extra(configs: set[str], dev, args) -> dict:
-    """Configs 3, 4 and 5, each timed with HIP events around its operator calls."""
+def time_rotated(fns, steps: int, warm: int, stream) -> float:
+    """time_op over calls that cycle through `fns` (independent copies of one
+    workload), so consecutive calls share no data through L2 or MALL."""
+    rot = iter(range(1 << 30))
+    return time_op(lambda: fns[next(rot) % len(fns)](), steps, warm, stream)[0]
+
+
+LONG_HISTORY = (131072, 524288, 1048576)
+
+
+def run_long_history(dev, steps: int, warm: int, stream) -> dict:
+    """Batch-1 decode over long histories, the reference's own benchmark
+    range (benchmarks/paged_attention/cpp/seq_len_vs_latency.cpp:47-55,
+    210-223 and python/test_paged_attention_python.py:140-141): 32 query / 16
+    kv heads, HD 128, bf16, 16-token pages (get_optimal_page_size), randomly
+    permuted pages; both split forms."""
+    out = {"workload": "batch-1 decode, 32/16 heads, HD 128, bf16, TPP 16, permuted pages; history lengths as in "
+                       "the reference's seq_len_vs_latency benchmark"}
+    for hist in LONG_HISTORY:
+        w = DecodeWorkload(30, num_seqs=1, ctx_lo=hist, ctx_hi=hist, hq=32, hkv=16, device=dev)
+        nbytes = w.decode_bytes()
+        rec = {"bytes": nbytes}
+        for part in (0, 512):
+            ms, _ = time_op(lambda: w.decode(part), steps, warm, stream)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            rec[f"partition_{part}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                        "tokens_per_s": round(1.0 / (ms * 1e-3), 1)}
+        out[f"history_{hist}"] = rec
+        del w
+        torch.cuda.empty_cache()
+    return out
+
+
+def run_extra(configs: set[str], dev, args, samples: dict | None = None) -> dict:
+    """Configs 3, 4 and 5 and the long-history points, each timed with HIP
+    events around its operator calls.  With `samples`, host copies of a
+    bounded subsample of each workload are kept for the CPU baseline."""
     out = {}
     stream = torch.cuda.current_stream(dev)
     steps, warm = max(1, args.extra_steps), 3
@@ -589,6 +690,14 @@ def run_extra(configs: set[str], dev, args) -> dict:
             gbs = nbytes / (ms * 1e-3) / 1e9
             res[f"partition_{part}"] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
                                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        if samples is not None:
+            s0 = int(np.argmin(w.lens_np))
+            kb, vb, spt = host_subset(w.k_pool, w.v_pool, w.pt_np, w.lens_np, [s0], w.tpp)
+            samples["c3"] = {"q": _host_bits(w.queries)[[s0]], "k": kb, "v": vb, "pt": spt, "lens": w.lens_np[[s0]],
+                             "dtype": "bf16", "bytes": nbytes,
+                             "scale": float(w.lens_np.sum()) / float(w.lens_np[s0]),
+                             "what": f"1 of 8 sequences ({int(w.lens_np[s0])} of {int(w.lens_np.sum())} context "
+                                     f"tokens), scaled by the token ratio"}
         w.make_fp8()
         f8 = w.decode_bytes_fp8()
         for part in (512, 0):
@@ -599,24 +708,43 @@ def run_extra(configs: set[str], dev, args) -> dict:
         del w
         torch.cuda.empty_cache()
     if "c4" in configs:
-        w = PrefillWorkload(dev)
-        fill_ms, _ = time_op(w.fill, steps, warm, stream)
-        att_ms, _ = time_op(w.attend, steps, warm, stream)
+        # three identical copies (same seed) in separate memory, cycled per
+        # call: each call's 0.2-0.4 GB working set then comes from HBM, not
+        # from the 256 MB last-level cache a repeated call would hit
+        ws = [PrefillWorkload(dev) for _ in range(3)]
+        w = ws[0]
+        fill_ms = time_rotated([x.fill for x in ws], steps, warm, stream)
+        att_ms = time_rotated([x.attend for x in ws], steps, warm, stream)
+        fill_hot_ms, _ = time_op(w.fill, steps, warm, stream)
         fl = w.flops()
         tf = fl / (att_ms * 1e-3) / 1e12
         out["prefill"] = {
             "workload": "config 4: 16 seqs, new U[512,2048] on cached U[0,2048], 32/8 heads, HD 128, bf16; "
-                        "fill_kv_pages of the new chunks, then causal attention (paged_attention, tile path)",
+                        "fill_kv_pages of the new chunks, then causal attention (paged_attention, tile path); "
+                        "timed over 3 rotated copies of the workload",
             "rows": w.rows, "causal_flops": fl,
             "attention_ms": round(att_ms, 4), "TFLOP/s": round(tf, 1),
             "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "fill_ms": round(fill_ms, 4), "fill_GB/s": round(w.fill_bytes() / (fill_ms * 1e-3) / 1e9, 1),
+            "fill_frac_of_hbm_peak": round(w.fill_bytes() / (fill_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "fill_same_copy_ms": round(fill_hot_ms, 4),
             "step_ms": round(att_ms + fill_ms, 4),
         }
+        if samples is not None:
+            s0 = int(np.argsort(w.new)[len(w.new) // 2])  # the median new chunk
+            lens = w.seq_lens.cpu().numpy()
+            kb, vb, spt = host_subset(w.k_pool, w.v_pool, w.page_table.cpu().numpy(), lens, [s0], 16)
+            rows = np.nonzero(w.q2seq.cpu().numpy() == s0)[0]
+            sfl = causal_flops(w.hq, w.hd, w.cached[[s0]], w.new[[s0]])
+            samples["c4"] = {"q": _host_bits(w.queries)[rows], "k": kb, "v": vb, "pt": spt, "lens": lens[[s0]],
+                             "q2s": np.zeros(len(rows), np.uint32), "off": w.q_offset.cpu().numpy()[rows],
+                             "dtype": "bf16", "flops": fl, "scale": fl / sfl,
+                             "what": f"1 of 16 sequences ({int(w.new[s0])} new rows on {int(w.cached[s0])} cached), "
+                                     f"scaled by the causal-flop ratio"}
         rope = RopeFill(w, dev)
         rope_ms, _ = time_op(rope.run, steps, warm, stream)
         out["prefill"]["rope_fill"] = rope.report(rope_ms)
-        del rope
+        del rope, ws[1:]
         # the same attention over fp8 e4m3 pools (per-(page, kv head) scales)
         k8, ks = to_fp8_pages(to_fp8_k_layout(w.k_pool))
         v8, vs = to_fp8_pages(w.v_pool)
@@ -626,7 +754,7 @@ def run_extra(configs: set[str], dev, args) -> dict:
         out["prefill"]["fp8_pages"] = {"attention_ms": round(f8_ms, 4), "TFLOP/s": round(f8_tf, 1),
                                        "frac_of_mfma_bf16_peak": round(f8_tf / MFMA_BF16_PEAK_TFLOPS, 4)}
         del k8, v8, ks, vs
-        del w
+        del w, ws
         torch.cuda.empty_cache()
         pw = PromptWorkload(dev)
         p_ms, _ = time_op(pw.attend, steps, warm, stream)
@@ -653,8 +781,34 @@ def run_extra(configs: set[str], dev, args) -> dict:
             "decode_rows_alone_ms": round(dec_ms, 4), "prefill_rows_alone_ms": round(pre_ms, 4),
             "ms_over_sum_of_halves": round(ms / (dec_ms + pre_ms), 4),
         }
+        if samples is not None:
+            lens = w.seq_lens.cpu().numpy()
+            q2s = w.q2seq.cpu().numpy()
+            off = w.q_offset.cpu().numpy()
+            pt = w.page_table.cpu().numpy()
+            qb = _host_bits(w.queries)
+            dec = list(range(0, 256, 16))  # 16 of the 256 decode sequences
+            kb, vb, spt = host_subset(w.k_pool, w.v_pool, pt, lens, dec, 16)
+            rows = np.nonzero(np.isin(q2s, dec))[0]
+            local = {s: i for i, s in enumerate(dec)}
+            dec_bytes = int(lens[dec].astype(np.int64).sum()) * 2 * 8 * 128 * 2
+            samples["c5d"] = {"q": qb[rows], "k": kb, "v": vb, "pt": spt, "lens": lens[dec],
+                              "q2s": np.array([local[int(x)] for x in q2s[rows]], np.uint32), "off": off[rows],
+                              "dtype": "f16", "bytes": w.decode_bytes, "scale": w.decode_bytes / dec_bytes,
+                              "what": "16 of the 256 decode rows, scaled by their share of the decode bytes"}
+            ch = 256 + int(np.argmax(lens[256:]))  # the chunk on the largest cache
+            kb, vb, spt = host_subset(w.k_pool, w.v_pool, pt, lens, [ch], 16)
+            rows = np.nonzero(q2s == ch)[0]
+            sfl = causal_flops(64, 128, np.array([lens[ch] - 1024]), np.array([1024]))
+            samples["c5p"] = {"q": qb[rows], "k": kb, "v": vb, "pt": spt, "lens": lens[[ch]],
+                              "q2s": np.zeros(len(rows), np.uint32), "off": off[rows], "dtype": "f16",
+                              "flops": w.prefill_flops, "scale": w.prefill_flops / sfl,
+                              "what": f"1 of the 4 prefill chunks (1024 rows on {int(lens[ch]) - 1024} cached), "
+                                      f"scaled by the causal-flop ratio"}
         del w
         torch.cuda.empty_cache()
+    if "lh" in configs:
+        out["long_history_decode"] = run_long_history(dev, min(steps, 10), warm, stream)
     return out
 
 

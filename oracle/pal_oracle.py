@@ -28,6 +28,10 @@ It restates, in numpy, what the reference computes on the hot path:
   pages (no reference counterpart: the reference stores f16 / bf16 only,
   paged_attention_kernels.metal:41-42); OCP e4m3 "fn" (bias 7, 3 mantissa
   bits, max 448, no infinities), round to nearest even.
+* ``torch_cpu_paged_attention`` -- the same decode / fused semantics as a
+  gather + torch scaled_dot_product_attention on the CPU (the reference's
+  equivalency path, decode/test_sdpa_equivalency.py:106-112), timed by
+  bench.py as the CPU baseline; pinned against the numpy functions above.
 * ``compaction_plan`` / ``apply_moves`` / ``remap_table`` -- the page-pool
   compaction (no reference counterpart); pinned by its invariants: the live
   set becomes [0, L), ids below L stay put, every page's bytes follow it,
@@ -525,6 +529,66 @@ def paged_attention(queries, k_pool, v_pool, page_table, seq_lens, q2seq, q_offs
         k, v = gather_tokens(kf, vf, pt[s], n)
         out[rows] = attend(q[rows], k, v, limits)
     return out
+
+
+# ---------------------------------------------------------------------------
+# the same computation on torch CPU (the CPU baseline's comparator)
+# ---------------------------------------------------------------------------
+
+
+def torch_cpu_paged_attention(queries, k_pool, v_pool, page_table, seq_lens, dtype, q2seq=None, q_offset=None):
+    """The reference's equivalency computation on torch CPU: gather each
+    sequence's pages (decode/test_sdpa_equivalency.py:141-173 inverted),
+    widen to float32, then torch's scaled_dot_product_attention with the GQA
+    map h -> h // (Hq / Hkv) and the row limits as a boolean mask.  Same
+    semantics as ``paged_attention`` (q2seq / q_offset given) or
+    ``paged_attention_decode`` (row s = sequence s, all its keys); returns
+    [R, Hq, HD] float32.  Used as the timed CPU baseline: its inputs are
+    raw 16-bit patterns already in host memory, as for the numpy oracle.
+    """
+    import torch
+
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    q = torch.from_numpy(np.ascontiguousarray(queries).view(np.int16)).view(tdt).float()
+    if q.dim() == 2:
+        q = q[:, None, :]
+    kp = torch.from_numpy(np.ascontiguousarray(k_pool).view(np.int16)).view(tdt)
+    vp = torch.from_numpy(np.ascontiguousarray(v_pool).view(np.int16)).view(tdt)
+    _, hkv, nstripe, tpp, x = kp.shape
+    hd = nstripe * x
+    pt = torch.from_numpy(np.asarray(page_table).astype(np.int64))
+    lens = np.asarray(seq_lens).astype(np.int64)
+    rows_n, hq, _ = q.shape
+    g = hq // hkv
+    if q2seq is None:
+        seqs = np.arange(pt.shape[0], dtype=np.int64)
+        offs = lens[: pt.shape[0]]
+    else:
+        seqs = np.asarray(q2seq).astype(np.int64)
+        offs = np.asarray(q_offset).astype(np.int64)
+    out = torch.zeros((len(seqs), hq, hd), dtype=torch.float32)
+    for s in np.unique(seqs):
+        if s >= pt.shape[0]:
+            continue
+        rows = np.nonzero(seqs == s)[0]
+        limits = np.minimum(lens[s], offs[rows])
+        n = int(max(0, limits.max()))
+        if n == 0:
+            continue
+        npg = (n + tpp - 1) // tpp
+        ids = pt[s, :npg]
+        # [pages, Hkv, HD/x, TPP, x] -> [tokens, Hkv, HD]; [pages, Hkv, HD, TPP] -> [tokens, Hkv, HD]
+        k = kp.index_select(0, ids).permute(0, 3, 1, 2, 4).reshape(npg * tpp, hkv, hd)[:n].float()
+        v = vp.index_select(0, ids).permute(0, 3, 1, 2).reshape(npg * tpp, hkv, hd)[:n].float()
+        qs = q[torch.from_numpy(rows)]                                   # [r, Hq, HD]
+        qh = qs.reshape(len(rows), hkv, g, hd).permute(1, 2, 0, 3).reshape(hkv, g * len(rows), hd)
+        lim = torch.from_numpy(np.tile(limits, g))                       # row order (head in group, row)
+        mask = torch.arange(n)[None, :] < lim[:, None]                   # [G*r, n]
+        o = torch.nn.functional.scaled_dot_product_attention(
+            qh[None], k.permute(1, 0, 2)[None], v.permute(1, 0, 2)[None], attn_mask=mask[None, None])[0]
+        o = torch.where((lim > 0)[None, :, None], o, torch.zeros(()))
+        out[torch.from_numpy(rows)] = o.reshape(hkv, g, len(rows), hd).permute(2, 0, 1, 3).reshape(len(rows), hq, hd)
+    return out.numpy()
 
 
 # ---------------------------------------------------------------------------

@@ -259,6 +259,32 @@ def test_fused_matches_decode_and_prefill():
     np.testing.assert_allclose(pre, ref, atol=3e-5, rtol=3e-5)
 
 
+def test_torch_cpu_restatement_matches_oracle():
+    """The CPU baseline's comparator (gather + torch SDPA on the CPU) equals
+    the numpy oracle: config 1 decode, a ragged GQA decode with NaN bits in
+    unused slots, and a fused batch of decode rows, prefill runs, an empty
+    row and a row naming no sequence."""
+    for dtype in DTYPES:
+        case = make_paged_case(0, [64, 100, 192, 256], 4, 1, 64, 16, dtype, extra_pages=25)
+        q = orc.f32_to_bits(np.random.default_rng(0).standard_normal((4, 4, 64)).astype(np.float32), dtype)
+        want = orc.paged_attention_decode(q, case.k_pool, case.v_pool, case.page_table, case.seq_lens, dtype)
+        got = orc.torch_cpu_paged_attention(q, case.k_pool, case.v_pool, case.page_table, case.seq_lens, dtype)
+        np.testing.assert_allclose(got, want, atol=2e-6, rtol=2e-6)
+    case = make_paged_case(5, [3, 700, 129, 1], 16, 4, 128, 32, "bf16")
+    q = orc.f32_to_bits(np.random.default_rng(5).standard_normal((4, 16, 128)).astype(np.float32), "bf16")
+    want = orc.paged_attention_decode(q, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "bf16")
+    got = orc.torch_cpu_paged_attention(q, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "bf16")
+    np.testing.assert_allclose(got, want, atol=2e-6, rtol=2e-6)
+    q2s = np.array([1, 1, 1, 0, 2, 2, 3, 9, 1], np.uint32)
+    off = np.array([5, 6, 7, 3, 100, 129, 0, 4, 700], np.int32)
+    qf = orc.f32_to_bits(np.random.default_rng(6).standard_normal((9, 16, 128)).astype(np.float32), "bf16")
+    want = orc.paged_attention(qf, case.k_pool, case.v_pool, case.page_table, case.seq_lens, q2s, off, "bf16")
+    got = orc.torch_cpu_paged_attention(qf, case.k_pool, case.v_pool, case.page_table, case.seq_lens, "bf16",
+                                        q2s, off)
+    np.testing.assert_allclose(got, want, atol=2e-6, rtol=2e-6)
+    assert not got[6].any() and not got[7].any()
+
+
 # ---------------------------------------------------------------------------
 # the checks above must catch plausible mistakes
 # ---------------------------------------------------------------------------
