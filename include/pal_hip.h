@@ -233,7 +233,10 @@ int pal_paged_attention_decode_noalloc(const void* queries, const void* k_pool, 
  * 1/sqrt(head_dim) (prefill.h.metal:147-234).  out: [num_query_rows *
  * num_q_heads, head_dim], row (s*P + i) * num_q_heads + h; rows at and past
  * num_seqs * P are not written.  head_dim % 32 == 0 (primitive :91-93).
- * No workspace.
+ * tokens_per_page: any multiple of 8 up to 1024, as the reference prefill
+ * reads it at run time (paged_attention_prefill.h.metal:243-263); 16 and 32
+ * have dedicated kernels, other sizes read their history keys through the
+ * registers (slower).  No workspace.
  */
 int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, const void* v_prompt,
                                 const void* k_cache_paged, const void* v_cache_paged, const uint32_t* page_table,
@@ -247,7 +250,7 @@ int pal_paged_attention_prefill(const void* q_prompt, const void* k_prompt, cons
  * the history's keys and values are their codes times the (page, kv head)
  * scales (k_scales / v_scales, fp32 [num_pages, Hkv]), dequantized to dtype
  * on the way into the tile; the dense prompt K/V and the queries are in
- * dtype.  head_dim 64, 128 or 256.
+ * dtype.  head_dim 64, 128 or 256; tokens_per_page 16 or 32.
  */
 int pal_paged_attention_prefill_fp8(const void* q_prompt, const void* k_prompt, const void* v_prompt,
                                     const void* k_cache_paged, const void* v_cache_paged, const float* k_scales,

@@ -61,6 +61,8 @@ bool decode_partition_ok(int partition_size) {
 
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
+constexpr int kMaxPageSize = 1024;  // prefill's run-time page sizes (multiples of 8)
+
 // Decode workspace layout (all offsets 256-aligned).  The claim counter at
 // byte 64 must be zero when a call starts; every call leaves it zero.  Every
 // other byte is scratch that each call writes before it reads.
@@ -151,7 +153,7 @@ pal::DecodeParams decode_params(const void* queries, const void* k_pool, const v
 
 // Checks shared by every attention entry point; returns PAL_OK or an error.
 int check_attention_dims(const char* op, int dtype, int num_q_heads, int num_kv_heads, int head_dim,
-                         int tokens_per_page, int64_t num_pages, int64_t page_table_width) {
+                         int tokens_per_page, int64_t num_pages, int64_t page_table_width, bool any_page_size = false) {
   if (!valid_dtype(dtype)) return fail(PAL_ERR_INVALID_ARGUMENT, "[%s] unsupported dtype code %d", op, dtype);
   if (num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || tokens_per_page <= 0 || num_pages < 0 ||
       page_table_width < 0)
@@ -159,8 +161,13 @@ int check_attention_dims(const char* op, int dtype, int num_q_heads, int num_kv_
   if (num_q_heads % num_kv_heads != 0)
     return fail(PAL_ERR_RUNTIME, "num_q_heads must be divisible by num_kv_heads (%d %% %d != 0)", num_q_heads,
                 num_kv_heads);
-  if (tokens_per_page != 16 && tokens_per_page != 32)
+  if (any_page_size) {  // prefill over 16-bit pools: any multiple of 8 up to kMaxPageSize
+    if (tokens_per_page % 8 != 0 || tokens_per_page > kMaxPageSize)
+      return fail(PAL_ERR_RUNTIME, "[%s] no kernel for tokens_per_page %d (supported: multiples of 8 up to %d)", op,
+                  tokens_per_page, kMaxPageSize);
+  } else if (tokens_per_page != 16 && tokens_per_page != 32) {
     return fail(PAL_ERR_RUNTIME, "[%s] no kernel for tokens_per_page %d (supported: 16, 32)", op, tokens_per_page);
+  }
   return PAL_OK;
 }
 
@@ -303,8 +310,10 @@ int prefill_call(const void* q_prompt, const void* k_prompt, const void* v_promp
                  int num_q_heads, int num_kv_heads, int head_dim, int tokens_per_page, int64_t num_pages,
                  int64_t page_table_width, hipStream_t stream) {
   const char* op = "paged_attention_prefill";
+  // 16-bit pools: any page size that is a multiple of 8 (the reference
+  // prefill reads it at run time); fp8 pools: 16 or 32
   int st = check_attention_dims(op, dtype, num_q_heads, num_kv_heads, head_dim, tokens_per_page, num_pages,
-                                page_table_width);
+                                page_table_width, k_scales == nullptr && v_scales == nullptr);
   if (st != PAL_OK) return st;
   st = check_fp8_scales(op, k_scales, v_scales, head_dim);
   if (st != PAL_OK) return st;
@@ -348,6 +357,7 @@ int prefill_call(const void* q_prompt, const void* k_prompt, const void* v_promp
   p.page_table_width = page_table_width;
   p.num_units = static_cast<int>(tiles);
   p.prompt_len = static_cast<int>(prompt_len);
+  p.tokens_per_page = tokens_per_page;
   p.num_q_heads = num_q_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = group;
@@ -441,6 +451,7 @@ int fused_call(const void* queries, const void* k_pool, const void* v_pool, cons
   pp.page_table_width = page_table_width;
   pp.num_units = static_cast<int>(windows);
   pp.prompt_len = 0;
+  pp.tokens_per_page = tokens_per_page;
   pp.num_q_heads = num_q_heads;
   pp.num_kv_heads = num_kv_heads;
   pp.group = group;

@@ -126,6 +126,7 @@ struct PrefillParams {
   int64_t page_table_width;
   int num_units;    // prompt mode: S * ceil(prompt_len / tokens per tile); window mode: ceil(R / tokens per tile)
   int prompt_len;   // > 0 selects uniform-prompt mode
+  int tokens_per_page;  // page size (the kernels built for 16 and 32 also take it as a constant)
   int num_q_heads;
   int num_kv_heads;
   int group;

@@ -48,12 +48,18 @@ hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Page sizes 16 and 32 have their own kernels; other multiples of 8 (16-bit
+// pools, uniform-prompt mode) run the kernel built for a run-time page size.
 template <int DT, int HD, bool KV8>
 hipError_t prefill_tpp(const PrefillParams& p, int tpp, hipStream_t stream) {
   switch (tpp) {
     case 16: return launch_prefill_t<DT, HD, 16, KV8>(p, stream);
     case 32: return launch_prefill_t<DT, HD, 32, KV8>(p, stream);
-    default: return hipErrorInvalidValue;
+    default:
+      if constexpr (!KV8) {
+        if (tpp > 0 && tpp % 8 == 0 && p.prompt_len > 0) return launch_prefill_t<DT, HD, 0, false>(p, stream);
+      }
+      return hipErrorInvalidValue;
   }
 }
 

@@ -140,19 +140,28 @@ template <int DT, int HD, int TPP, bool PROMPT, bool KV8>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, int nrows, int64_t s, int kvh, int h0,
                                              uint16_t* k_lds_base, uint16_t* v_lds_base, uint16_t* junk_lds,
                                              uint32_t* pid_lds, int* lim_lds, float* scl_lds) {
+  // TPP 0: the page size is p.tokens_per_page, known at run time (a
+  // multiple of 8; the reference prefill takes any, paged_attention_prefill.h.metal:
+  // 243-263).  Steps of history keys then take the register path, reading
+  // each key's page id from the page table; steps of dense prompt keys are
+  // copied as for the other page sizes.  LDS holds every step in the
+  // 32-key-page item order.
+  constexpr int TP = TPP == 0 ? 32 : TPP;  // page size of the LDS item order
+  const int tpp = TPP == 0 ? p.tokens_per_page : TPP;
+  static_assert(TPP != 0 || (PROMPT && !KV8), "run-time page sizes: uniform-prompt mode, 16-bit pools");
   static_assert(HD % 32 == 0, "prefill needs head_dim % 32 == 0");
   static_assert(2 * StepGeo<HD>::kLoads <= HD / 16, "a step's copies fit in its PV chunks");
   constexpr int KS = HD / 16;  // QK k-steps of 16
   constexpr int DT32 = HD / 32;  // O^T row tiles of 32 dims
   constexpr int NI = StepGeo<HD>::kItems;
   constexpr int NL = StepGeo<HD>::kLoads;
-  using IM = ItemMap<HD, TPP>;
+  using IM = ItemMap<HD, TP>;
   // fp8 pools in window mode: steps are copied as fp8 bytes (16-byte items:
   // 16 dims of one key for K, 16 keys of one row for V; 2 HD items each, in
   // item order) and converted in the operand reads.  A copy instruction must
-  // stay in one page: with TPP 16 that needs HD % 64 == 0 (every fp8 pool's
+  // stay in one page: with TP 16 that needs HD % 64 == 0 (every fp8 pool's
   // head dim).
-  constexpr bool F8 = KV8 && !PROMPT && (TPP == 32 || HD % 64 == 0);
+  constexpr bool F8 = KV8 && !PROMPT && (TP == 32 || HD % 64 == 0);
   constexpr int NI8 = 2 * HD;
   constexpr int NL8 = (NI8 + kPfThreads - 1) / kPfThreads;
   constexpr int NC = F8 ? NL8 : NL;  // copies per thread per step, K (and V)
@@ -176,7 +185,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   const int col = lane & 31;  // this lane's M-row within the wave
   const int half = lane >> 5;
 
-  const int64_t max_tokens = p.page_table_width * TPP;
+  const int64_t max_tokens = p.page_table_width * tpp;
   int64_t hist = 0;  // prompt mode: keys below hist come from pages
   int64_t slen;
   if (prompt_mode) {
@@ -262,7 +271,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   const int min_lim = __builtin_amdgcn_readfirstlane(lim_lds[kMRows + 1]);
   const int my_lim = lim_lds[m_row];
 
-  const int64_t head_block = static_cast<int64_t>(HD) * TPP;
+  const int64_t head_block = static_cast<int64_t>(HD) * tpp;
   const int64_t page_stride = head_block * p.num_kv_heads;
   const int64_t page_stride8 = page_stride;            // fp8 pools: bytes per page (one byte per element)
   const int64_t kv_head_off8 = kvh * head_block;       // and of a kv head's block
@@ -273,7 +282,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // page-table entries the tile reads: keys below max_lim, and in prompt mode
   // only those below the history (the rest are dense) -- never past the width
   const int paged_keys = prompt_mode ? min(max_lim, static_cast<int>(hist)) : max_lim;
-  const int n_pid = (paged_keys + TPP - 1) / TPP;
+  const int n_pid = TPP == 0 ? 0 : (paged_keys + TP - 1) / TP;  // runtime page size: no staged ids
 
   // Page ids live in LDS (two chunks of 512 entries, entry e in slot e % 1024):
   // reading them is an LDS broadcast, so the only vector-memory traffic in the
@@ -305,7 +314,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // Slow step (invalid pages, history / prompt boundary, fp8 in prompt mode): register loads,
   // masked, then LDS stores -- synchronous, so it also drains the copies in
   // flight, which keeps the counted waits safe.
-  // pg0 / pg1: the pages of the step's first and (TPP 16) second 16 keys.
+  // pg0 / pg1: the pages of the step's first and (TP 16) second 16 keys.
   constexpr bool kAllItems = NI % kPfThreads == 0;  // no wavefront has a padding copy
   __builtin_assume(w >= 0 && w < kPfWaves);
   // page ids >= 2^32 - 1 cannot occur with fewer pages; such an id takes the slow path
@@ -326,15 +335,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       const uint16_t* page = p.v_pool + (IM::k_page_half(ok ? ib : 0) ? off1 : off0);
       int d = 0, key = 0;
       if (ok) IM::v_item(i, d, key);
-      const uint32_t src = 2u * static_cast<uint32_t>(d * TPP + key % TPP);
+      const uint32_t src = 2u * static_cast<uint32_t>(d * TP + key % TP);
       copy_to_lds16(page, src, lds_addr(ok ? v_lds(buf) + ib * 8 : junk_lds));
     }
   };
-  // fp8 items.  K item i: page half ph (TPP 16), stripe c (dims 16c ..
-  // 16c+15), key of the step; V item i: page half ph (TPP 16) or 16-key half
-  // of the page row (TPP 32), row d.  Item i is LDS slot i.
+  // fp8 items.  K item i: page half ph (TP 16), stripe c (dims 16c ..
+  // 16c+15), key of the step; V item i: page half ph (TP 16) or 16-key half
+  // of the page row (TP 32), row d.  Item i is LDS slot i.
   auto k8_item = [](int i, int& ph, int& c, int& key) {
-    if (TPP == 16) {
+    if (TP == 16) {
       ph = i / HD;
       c = (i % HD) / 16;
       key = 16 * ph + i % 16;
@@ -345,7 +354,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     }
   };
   auto v8_item = [](int i, int& ph, int& d, int& kb) {  // kb: the item's first key in the step
-    if (TPP == 16) {
+    if (TP == 16) {
       ph = i / HD;
       d = i % HD;
       kb = 16 * ph;
@@ -368,12 +377,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     uint32_t src = 0;
     if (q < NL8) {
       if (ok) k8_item(i, ph, a, b);
-      src = static_cast<uint32_t>((a * TPP + b % TPP) * 16);
+      src = static_cast<uint32_t>((a * TP + b % TP) * 16);
     } else {
       if (ok) v8_item(i, ph, a, b);
-      src = static_cast<uint32_t>(a * TPP + b % TPP);
+      src = static_cast<uint32_t>(a * TP + b % TP);
     }
-    const int phw = (TPP == 16 && ok) ? ib / HD : 0;  // the load's page half (one page per instruction)
+    const int phw = (TP == 16 && ok) ? ib / HD : 0;  // the load's page half (one page per instruction)
     const uint8_t* page = (q < NL8 ? k8_pool : v8_pool) + (phw ? boff1 : boff0);
     copy_to_lds16(page, ok ? src : 0u, lds_addr(ok ? (q < NL8 ? k_lds(buf) : v_lds(buf)) + ib * 8 : junk_lds));
   };
@@ -394,7 +403,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         u32x4 val = {0u, 0u, 0u, 0u};
         if (pg < p.num_pages && k0 + key < max_lim)
           val = *reinterpret_cast<const u32x4*>(k8_pool + static_cast<int64_t>(pg) * page_stride8 +
-                                                (c * TPP + key % TPP) * 16);
+                                                (c * TP + key % TP) * 16);
         *reinterpret_cast<u32x4*>(k_lds(buf) + i * 8) = val;
       }
       {
@@ -404,7 +413,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         u32x4 val = {0u, 0u, 0u, 0u};
         const int valid = max_lim - (k0 + kb);
         if (pg < p.num_pages && valid > 0) {
-          val = *reinterpret_cast<const u32x4*>(v8_pool + static_cast<int64_t>(pg) * page_stride8 + d * TPP + kb % TPP);
+          val = *reinterpret_cast<const u32x4*>(v8_pool + static_cast<int64_t>(pg) * page_stride8 + d * TP + kb % TP);
 #pragma unroll
           for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -421,7 +430,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // no row sees, from valid pages, and fix_tail clears their V entries)
   auto is_fast = [&](int j, uint32_t pg0, uint32_t pg1) {
     const int k0 = j * kKeys;
-    return (!KV8 || F8) && k0 < max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
+    return TPP != 0 && (!KV8 || F8) && k0 < max_lim && pg0 < np32 && pg1 < np32 && (!prompt_mode || k0 + kKeys <= hist);
   };
   // Prompt mode: a step whose 32 keys are all prompt keys below the tile's
   // largest limit copies them from the dense prompt rows (16-bit in every
@@ -469,7 +478,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       for (int q = 0; q < 2 * NL; ++q) copy_dense(q, buf, j);
       return;
     }
-    if (TPP != 16) pg1 = pg0;
+    if (TP != 16) pg1 = pg0;
     const bool fast = is_fast(j, pg0, pg1);
     if constexpr (F8) {
       if (fast) {
@@ -486,6 +495,72 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       const int64_t off1 = static_cast<int64_t>(pg1) * page_stride + kv_head_off;
 #pragma unroll
       for (int q = 0; q < 2 * NL; ++q) copy_one(q, buf, off0, off1);
+      return;
+    }
+    if constexpr (TPP == 0) {
+      // run-time page size: each key's page from the page table (8 keys
+      // of a V group share a page: the size is a multiple of 8)
+#pragma unroll
+      for (int jj = 0; jj < NL; ++jj) {
+        const int i = tid + jj * kPfThreads;
+        if (i >= NI) continue;
+        {
+          int kj, c;
+          IM::k_item(i, c, kj);
+          const int tok = k0 + kj;
+          u32x4 val = {0u, 0u, 0u, 0u};
+          if (tok < max_lim) {
+            if (tok < hist) {
+              const uint32_t pg = pt[tok / tpp];
+              PAL_DEBUG_FLAG(pg >= p.num_pages, kDebugPageId);
+              if (pg < p.num_pages)
+                val = *reinterpret_cast<const u32x4*>(p.k_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off +
+                                                      (static_cast<int64_t>(c) * tpp + tok % tpp) * 8);
+            } else {
+              val = *reinterpret_cast<const u32x4*>(p.k_dense + (dense_row0 + tok) * dense_stride + kvh * HD + c * 8);
+            }
+          }
+          *reinterpret_cast<u32x4*>(k_lds(buf) + i * 8) = val;
+        }
+        {
+          int d, key;
+          IM::v_item(i, d, key);
+          const int tok = k0 + key;
+          u32x4 val = {0u, 0u, 0u, 0u};
+          if (tok < max_lim) {
+            const uint32_t pg = tok < hist ? pt[tok / tpp] : 0u;
+            const bool pg_ok = pg < p.num_pages;
+            const uint16_t* vrow = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off +
+                                   static_cast<int64_t>(d) * tpp + tok % tpp;
+            if (tok + 8 <= hist) {
+              if (pg_ok) val = *reinterpret_cast<const u32x4*>(vrow);
+            } else {
+              uint32_t e16[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const int t2 = tok + e;
+                uint16_t x = 0;
+                if (t2 < max_lim) {
+                  if (t2 >= hist)
+                    x = p.v_dense[(dense_row0 + t2) * dense_stride + kvh * HD + d];
+                  else if (pg_ok)
+                    x = vrow[e];
+                }
+                e16[e] = x;
+              }
+              val = {e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16),
+                     e16[6] | (e16[7] << 16)};
+            }
+            const int valid = max_lim - tok;  // keys past the largest limit may hold anything
+            if (valid < 8) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                val[e] &= (2 * e < valid ? 0x0000FFFFu : 0u) | (2 * e + 1 < valid ? 0xFFFF0000u : 0u);
+            }
+          }
+          *reinterpret_cast<u32x4*>(v_lds(buf) + i * 8) = val;
+        }
+      }
       return;
     }
 #pragma unroll
@@ -506,7 +581,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
           if (pg_ok && tok < max_lim) {
             if constexpr (KV8) {  // dims 8c..8c+7: half of 16-dim stripe c / 2, times the page's K scale
               const uint8_t* kp8 = reinterpret_cast<const uint8_t*>(p.k_pool) + static_cast<int64_t>(pg) * page_stride8 +
-                                   kv_head_off8 + ((c >> 1) * TPP + kj % TPP) * 16 + (c & 1) * 8;
+                                   kv_head_off8 + ((c >> 1) * TP + kj % TP) * 16 + (c & 1) * 8;
               val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(kp8),
                                      p.k_scales[static_cast<int64_t>(pg) * p.num_kv_heads + kvh]);
             } else {
@@ -524,17 +599,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         int d, key;
         IM::v_item(i, d, key);
         const int tok = k0 + key;
-        const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off + d * TPP;
+        const uint16_t* vpage = p.v_pool + static_cast<int64_t>(pg) * page_stride + kv_head_off + d * TP;
         const uint8_t* vpage8 = reinterpret_cast<const uint8_t*>(p.v_pool) + static_cast<int64_t>(pg) * page_stride8 +
-                                kv_head_off8 + d * TPP;
+                                kv_head_off8 + d * TP;
         const float vsc = KV8 && pg_ok ? p.v_scales[static_cast<int64_t>(pg) * p.num_kv_heads + kvh] : 1.f;
         u32x4 val = {0u, 0u, 0u, 0u};
         if (!prompt_mode || tok + 8 <= hist) {
           if (pg_ok && tok < max_lim) {
             if constexpr (KV8) {
-              val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(vpage8 + key % TPP), vsc);
+              val = fp8x8_scaled<DT>(*reinterpret_cast<const u32x2*>(vpage8 + key % TP), vsc);
             } else {
-              val = *reinterpret_cast<const u32x4*>(vpage + key % TPP);
+              val = *reinterpret_cast<const u32x4*>(vpage + key % TP);
             }
           }
         } else if (tok < max_lim) {
@@ -549,10 +624,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
               if (!pgd) {
                 x = p.v_dense[(dense_row0 + t2) * dense_stride + kvh * HD + d];
               } else if constexpr (KV8) {
-                const uint32_t code = vpage8[(key + e) % TPP];
+                const uint32_t code = vpage8[(key + e) % TP];
                 x = static_cast<uint16_t>(fp8x8_scaled<DT>(u32x2{code, 0u}, vsc)[0] & 0xFFFFu);
               } else {
-                x = vpage[(key + e) % TPP];
+                x = vpage[(key + e) % TP];
               }
             }
             e16[e] = x;
@@ -626,15 +701,15 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     }
   };
   const bool tail_partial = max_lim % kKeys != 0;  // the last step ends past max_lim
-  // the page ids of step j (an LDS broadcast read; TPP 32: one page)
-  // fp8: the scales of step j's first and (TPP 16) second page (LDS
+  // the page ids of step j (an LDS broadcast read; TP 32: one page)
+  // fp8: the scales of step j's first and (TP 16) second page (LDS
   // broadcast); 0 for a page past the tile's last staged entry (the tail
   // step's keys past max_lim: their V bytes are cleared, and 0 x a stale
   // scale could be NaN)
   auto read_scales = [&](const float* arr, int j, float& s0, float& s1) {
-    const int e = j * kKeys / TPP;
+    const int e = j * kKeys / TP;
     s0 = e < n_pid ? arr[e % (2 * kPidChunk)] : 0.f;
-    s1 = TPP == 16 ? (e + 1 < n_pid ? arr[(e + 1) % (2 * kPidChunk)] : 0.f) : s0;
+    s1 = TP == 16 ? (e + 1 < n_pid ? arr[(e + 1) % (2 * kPidChunk)] : 0.f) : s0;
   };
   // fp8: step j's scores times the K scale of each key's page (register r
   // holds key 16 (r / 8) + ..., so r < 8: the first page)
@@ -647,9 +722,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     }
   };
   auto read_pids = [&](int j) {
-    const int e = (j * kKeys / TPP) % (2 * kPidChunk);
+    const int e = (j * kKeys / TP) % (2 * kPidChunk);
     u32x2 v;
-    if (TPP == 16) {
+    if (TP == 16) {
       v = *reinterpret_cast<const u32x2*>(pid_lds + e);  // e is even: 8-byte aligned
     } else {
       v.x = pid_lds[e];
@@ -679,7 +754,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       const uint8_t* kb = reinterpret_cast<const uint8_t*>(k_lds(buf));
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        const int slot = TPP == 16 ? (key / 16) * HD + kk * 16 + key % 16 : kk * 32 + key;
+        const int slot = TP == 16 ? (key / 16) * HD + kk * 16 + key % 16 : kk * 32 + key;
         ka[kk] = fp8x8_exact<DT>(*reinterpret_cast<const u32x2*>(kb + slot * 16 + 8 * half));
       }
       return;
@@ -836,7 +911,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       } else if constexpr (F8) {  // row d = col + 32 (kk % DT32), keys 16 g + 8 half .. +7 of item (g, d)
         const int g = kk / DT32;
         const int d = col + 32 * (kk % DT32);
-        const int slot = TPP == 16 ? g * HD + d : d * 2 + g;
+        const int slot = TP == 16 ? g * HD + d : d * 2 + g;
         // exact in 16 bits; the V scale is on P.  Chunk kk converts the
         // operand read in chunk kk - 1 (its LDS read has landed by then) and
         // consumes it there, so the conversions are not sunk to the PV MFMAs.
@@ -854,7 +929,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
       for (int q = kk * 8 / KS; q < (kk + 1) * 8 / KS; ++q) {
         if constexpr (F8) {  // the exp-sum of the probabilities, then P times its key's page V scale
-          const float sv = (TPP == 16 && q >= 4) ? vs1 : vs0;
+          const float sv = (TP == 16 && q >= 4) ? vs1 : vs0;
           l_run += pe[2 * q] + pe[2 * q + 1];
           pp[q] = Dt<DT>::pack2(pe[2 * q] * sv, pe[2 * q + 1] * sv);
         } else {
@@ -878,7 +953,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
     // memory pipeline (measured 3 % on config 4 against issuing them all
     // after the chunks); other steps take the synchronous path below.
     const uint32_t jp0 = __builtin_amdgcn_readfirstlane(pgv.x);
-    const uint32_t jp1 = TPP == 16 ? __builtin_amdgcn_readfirstlane(pgv.y) : jp0;
+    const uint32_t jp1 = TP == 16 ? __builtin_amdgcn_readfirstlane(pgv.y) : jp0;
     const bool jdense = j < nsteps && (vdense || is_dense(j));  // steps after a dense one are dense
     const bool jfast = j < nsteps && (jdense || is_fast(j, jp0, jp1));
     const int64_t joff0 = static_cast<int64_t>(jp0) * page_stride + kv_head_off;
@@ -911,7 +986,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       // entering page-id chunk q (q >= 1): stage chunk q + 1 over chunk q - 1,
       // whose last reader finished before this iteration's barrier; the next
       // barriers publish it long before its first reader
-      const int e0 = j * kKeys / TPP;
+      const int e0 = j * kKeys / TP;
       if (e0 % kPidChunk == 0 && e0 > 0 && e0 + kPidChunk < n_pid) stage_pids(e0 / kPidChunk + 1);
       if (!jfast) issue(j, jp0, jp1);
     }
@@ -1006,22 +1081,24 @@ __device__ __forceinline__ void prefill_block(const PrefillParams& p, unsigned b
       return;
     }
   }
-  // windows in reverse row order: a sequence's later rows see more keys, so
-  // its longest tiles start first and the grid ends on short ones
-  const int w0 = (p.num_units - 1 - unit) * qt;
-  const int w1 = static_cast<int>(min(static_cast<int64_t>(w0 + qt), p.num_rows));
-  const int tid = threadIdx.x;
-  if (tid < w1 - w0) run_start[tid] = (tid == 0 || p.q2seq[w0 + tid] != p.q2seq[w0 + tid - 1]) ? 1 : 0;
-  __syncthreads();
-  int cur = w0;
-  while (cur < w1) {
-    int end = cur + 1;
-    while (end < w1 && !run_start[end - w0]) ++end;
-    end = __builtin_amdgcn_readfirstlane(end);
-    if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
-      prefill_tile<DT, HD, TPP, false, KV8>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
-                                       lim_lds, scl_lds);
-    cur = end;
+  if constexpr (TPP != 0) {  // run-time page sizes: uniform-prompt mode only
+    // windows in reverse row order: a sequence's later rows see more keys, so
+    // its longest tiles start first and the grid ends on short ones
+    const int w0 = (p.num_units - 1 - unit) * qt;
+    const int w1 = static_cast<int>(min(static_cast<int64_t>(w0 + qt), p.num_rows));
+    const int tid = threadIdx.x;
+    if (tid < w1 - w0) run_start[tid] = (tid == 0 || p.q2seq[w0 + tid] != p.q2seq[w0 + tid - 1]) ? 1 : 0;
+    __syncthreads();
+    int cur = w0;
+    while (cur < w1) {
+      int end = cur + 1;
+      while (end < w1 && !run_start[end - w0]) ++end;
+      end = __builtin_amdgcn_readfirstlane(end);
+      if (end - cur > 1 || !single_row(p.q2seq, cur, p.num_rows))
+        prefill_tile<DT, HD, TPP, false, KV8>(p, cur, end - cur, p.q2seq[cur], kvh, h0, k_lds, v_lds, junk_lds, pid_lds,
+                                         lim_lds, scl_lds);
+      cur = end;
+    }
   }
 }
 

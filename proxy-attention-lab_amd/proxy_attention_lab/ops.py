@@ -529,9 +529,12 @@ def paged_attention_prefill(
     Prompt token i of sequence s attends to the cached tokens
     [0, context_len_arr[s]) of its pages and to prompt tokens 0..i.
     Returns [N * Hq, HD], row (s*P + i) * Hq + h; rows past S*P (when N is
-    not a multiple of S) are zero.  HD % 32 == 0.  The prompt's K/V need not
-    be in the pages.  fp8 history pools (an addition) need ``k_scales`` /
-    ``v_scales`` (float32 [num_pages, Hkv]); head_dim 64, 128 or 256.
+    not a multiple of S) are zero.  HD % 32 == 0.  The page size may be any
+    multiple of 8 up to 1024, as in the reference (prefill.h.metal:243-263);
+    16 and 32 have dedicated kernels, other sizes read the history through
+    registers (slower).  The prompt's K/V need not be in the pages.  fp8
+    history pools (an addition) need ``k_scales`` / ``v_scales`` (float32
+    [num_pages, Hkv]); head_dim 64, 128 or 256, page size 16 or 32.
     """
     op = "paged_attention_prefill"
     _require_device("q_prompt", q_prompt)

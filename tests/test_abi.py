@@ -120,7 +120,12 @@ def test_prefill_rejects_bad_arguments_without_launch():
     assert call(hq=6, hkv=4) == _lib.PAL_ERR_RUNTIME and "divisible" in _lib.last_error()
     assert call(hd=80) == _lib.PAL_ERR_RUNTIME and "32" in _lib.last_error()  # prefill_primitive.cpp:91-93
     assert call(hd=160) == _lib.PAL_ERR_RUNTIME  # no kernel
-    assert call(tpp=8) == _lib.PAL_ERR_RUNTIME
+    # any page size that is a multiple of 8 (up to 1024) passes the checks
+    # (here it then stops at the null pointers); others have no kernel
+    for tpp in (8, 24, 56, 64, 1024):
+        assert call(tpp=tpp) == _lib.PAL_ERR_INVALID_ARGUMENT and "null" in _lib.last_error()
+    for tpp in (4, 12, 20, 1032):
+        assert call(tpp=tpp) == _lib.PAL_ERR_RUNTIME and "multiples of 8" in _lib.last_error()
     assert call(dtype=7) == _lib.PAL_ERR_INVALID_ARGUMENT
     assert call() == _lib.PAL_ERR_INVALID_ARGUMENT and "null" in _lib.last_error()
     assert call(seqs=0) == 0  # nothing to do

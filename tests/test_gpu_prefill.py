@@ -135,3 +135,19 @@ def test_prefill_dense_prompt_steps(hd, dtype):
     back with transposing LDS reads), after paged steps of histories that end
     on and off a step boundary."""
     _check(70 + hd, [0, 64, 96, 31, 33], 160, 16, 4, hd, 16, dtype, f"dense prompt steps hd{hd}")
+
+
+# The reference prefill reads the page size at run time
+# (paged_attention_prefill.h.metal:243-263); 16 and 32 have their own kernels,
+# other multiples of 8 (including the 56 of the reference's C++ benchmark,
+# seq_len_vs_latency.cpp:47-55) run the run-time page-size kernel.
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("tpp", [8, 24, 56, 64, 128])
+def test_prefill_runtime_page_sizes(tpp, dtype):
+    _check(tpp, [0, 1, 7, 8, 9, tpp - 1, tpp, tpp + 1, 300, 1000], 37, 16, 4, 128, tpp, dtype, f"tpp{tpp}")
+
+
+@pytest.mark.parametrize("hd", [32, 64, 96, 256])
+def test_prefill_runtime_page_size_head_dims(hd):
+    _check(hd + 1, [5, 40, 0, 129], 45, 8, 2, hd, 8, "bf16", f"tpp8 hd{hd}")
+    _check(hd + 2, [5, 40, 0, 129], 45, 8, 2, hd, 64, "f16", f"tpp64 hd{hd}")
