@@ -456,19 +456,19 @@ def cpu_baseline(samples: dict) -> dict:
     t1 = run(c1, 20, 3)
     res["config1"] = {"ms": round(t1 * 1e3, 3), "sample": "config 1 in full (4 sequences)"}
     c2 = samples["c2"]
-    t2 = run(c2, 10, 3)
+    t2 = run(c2, 40, 3)
     res["value"] = round(c2["bytes"] / t2 / 1e9, 3)
     res["tokens_per_s"] = round(len(c2["lens"]) / t2, 2)
     res["config2_ms"] = round(t2 * 1e3, 2)
     res["sample"] = (f"config 2 in full (64 sequences, {int(c2['lens'].sum())} context tokens, the same pools as "
                      f"the GPU run's first copy): decode by gather + torch fp32 scaled_dot_product_attention, "
-                     f"median of 10 after 3 warm-up; the fill step not included")
+                     f"median of 40 after 3 warm-up; the fill step not included")
     for key, name in (("c3", "config3"), ("c4", "config4"), ("c5d", "config5_decode_rows"),
                       ("c5p", "config5_prefill_rows")):
         sm = samples.get(key)
         if sm is None:
             continue
-        t = run(sm, 3, 1)
+        t = run(sm, 8, 1)
         rec = {"sample": sm["what"], "ms_sample": round(t * 1e3, 2), "scale": round(sm["scale"], 3),
                "ms_scaled": round(t * sm["scale"] * 1e3, 1)}
         if "bytes" in sm:
