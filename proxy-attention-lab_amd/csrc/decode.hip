@@ -348,6 +348,9 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     PAL_FIND_PIECE(c_, s0, b0 - cum[s0], b0, c_vend);
   }
   load_q(c_s, c_seg, qv4, qv2);
+  // fp8 pools: the query as fp8 terms, the B operand of the fp8 MFMA
+  QueryFp8<DT, KV8 ? KK : 1> q8;
+  if constexpr (KV8) query_to_fp8<DT, KK>(qv4, q8);
 
   // Page ids in register windows of 64 pages (one id per lane): pid_cur
   // holds window wcur, the window of the block being computed, and pid_nxt
@@ -373,7 +376,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   bool has_next = false;
   x_s = c_s; x_r = c_r; x_gpos = c_gpos; x_seq = c_seq; x_len = c_len; x_nb = c_nb; x_blk = c_blk;
   x_count = c_count; x_seg = c_seg;
-  uint32_t pidn0 = 0;  // window 0 of the next piece
+  uint32_t pidn0 = 0;  // window 0 of the next piece (a load in flight)
+  // pidn0 once it has arrived: a copy made after the exact wait at the end of
+  // a step group, so the issues of later groups select from it without
+  // waiting on the load
+  uint32_t pidn0_ready = 0;
 
   for (;;) {
     const int kvh = c_seg / p.head_chunks;
@@ -403,14 +410,14 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     // block is read exactly once per call, so the loads carry the
     // non-temporal hint: the stream does not displace other lines (page ids,
     // partials, the fused op's prefill tiles) from L2 and MALL.
-    auto issue = [&](int64_t i, int buf) {
+    auto issue = [&](int64_t i, int buf, uint32_t w_n0) {
       const bool to_next = has_next && i >= n_pad;
       const int64_t j = to_next ? (i - n_pad < nblk_n - 1 ? i - n_pad : nblk_n - 1) : (i < n_blk - 1 ? i : n_blk - 1);
       const int64_t b = (to_next ? bstart_n : bstart) + j;
       const int64_t e = (b * 16) / TPP - (to_next ? pbase_n : pbase);  // page within the piece's windows
       // (selects of values, not of variables: a select of two variables'
       // addresses would push the whole pipeline state to scratch)
-      const uint32_t w_n0 = pidn0, w_c = pid_cur, w_x = pid_nxt;
+      const uint32_t w_c = pid_cur, w_x = pid_nxt;
       const uint32_t win = to_next ? w_n0 : ((e >> 6) == wcur ? w_c : w_x);
       const uint32_t pg = __builtin_amdgcn_readlane(win, static_cast<int>(e & 63));
       bv[buf] = pg < p.num_pages;
@@ -464,16 +471,17 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       const bool live = bv[buf] && i < n_blk;  // steps past the piece end are fully masked
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       if constexpr (KV8) {
-        // 16 fp8 values (one stripe) -> two 8-element operands, exactly
+        // the K codes as loaded are the A operand (stripes g + 8m and
+        // g + 8m + 4, 32 bytes), the query's fp8 terms the B operand
 #pragma unroll
-        for (int j = 0; j < KL8; ++j) {
-          const u32x4 w = kb4[buf][j];
-          const u32x4 lo = {Dt<DT>::fp8x2(w.x, false), Dt<DT>::fp8x2(w.x, true), Dt<DT>::fp8x2(w.y, false),
-                            Dt<DT>::fp8x2(w.y, true)};
-          const u32x4 hi = {Dt<DT>::fp8x2(w.z, false), Dt<DT>::fp8x2(w.z, true), Dt<DT>::fp8x2(w.w, false),
-                            Dt<DT>::fp8x2(w.w, true)};
-          acc = Dt<DT>::mma16x16x32(lo, qv4[2 * j], acc);
-          acc = Dt<DT>::mma16x16x32(hi, qv4[2 * j + 1], acc);
+        for (int m = 0; m < q8.kOps; ++m) {
+          const u32x4 a0 = kb4[buf][2 * m];
+          const u32x4 a1 = 2 * m + 1 < KL8 ? kb4[buf][2 * m + 1] : u32x4{0u, 0u, 0u, 0u};
+          const i32x8 a = {static_cast<int>(a0.x), static_cast<int>(a0.y), static_cast<int>(a0.z),
+                           static_cast<int>(a0.w), static_cast<int>(a1.x), static_cast<int>(a1.y),
+                           static_cast<int>(a1.z), static_cast<int>(a1.w)};
+#pragma unroll
+          for (int t = 0; t < q8.kTerms; ++t) acc = mma_fp8_16x16x128(a, q8.w[t][m], acc, q8.s_hi - 4 * t);
         }
         acc *= bks[buf];  // the block's K scale
       } else {
@@ -486,17 +494,19 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
           }
         }
       }
-      // tokens past the end (and whole invalid blocks) are masked
-      const int64_t t0 = live ? b * 16 + 4 * g : len;
+      // tokens past the end (and whole invalid blocks) are masked: token
+      // 4g + e of the block is a key when e < kl (the block's key count is
+      // uniform, so the 64-bit part is scalar)
+      const int64_t left = live ? len - b * 16 : 0;
+      const int kl = static_cast<int>(left < 16 ? left : 16) - 4 * g;
       float sc4[4];
       float bm = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        sc4[e] = (t0 + e < len) ? acc[e] : -INFINITY;
+        sc4[e] = e < kl ? acc[e] : -INFINITY;
         bm = fmaxf(bm, sc4[e]);
       }
-      bm = fmaxf(bm, shfl_xor(bm, 16));
-      bm = fmaxf(bm, shfl_xor(bm, 32));
+      bm = max_xor32(max_xor16(bm));  // over the 4 lane groups (scores are finite or -inf)
       const float m_new = fmaxf(m_run, bm);
       const float msc = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
       if (__ballot(m_new > m_run && m_run != -INFINITY)) {
@@ -517,18 +527,19 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       const float pvs = KV8 ? bvs[buf] : 1.f;
       const u32x2 pb = {Dt<DT>::pack2(pe[0] * pvs, pe[1] * pvs), Dt<DT>::pack2(pe[2] * pvs, pe[3] * pvs)};
       // slots past the end may hold anything, NaN bits included: zero their
-      // V (branch-free: two ANDs per tile)
-      const uint32_t mlo = (t0 < len ? 0x0000FFFFu : 0u) | (t0 + 1 < len ? 0xFFFF0000u : 0u);
-      const uint32_t mhi = (t0 + 2 < len ? 0x0000FFFFu : 0u) | (t0 + 3 < len ? 0xFFFF0000u : 0u);
+      // V (branch-free: two ANDs per tile, or one on the fp8 codes)
+      const uint32_t mlo = (kl > 0 ? 0x0000FFFFu : 0u) | (kl > 1 ? 0xFFFF0000u : 0u);
+      const uint32_t mhi = (kl > 2 ? 0x0000FFFFu : 0u) | (kl > 3 ? 0xFFFF0000u : 0u);
+      const uint32_t m8 = kl >= 4 ? 0xFFFFFFFFu : (kl <= 0 ? 0u : (0xFFFFFFFFu >> (32 - 8 * kl)));
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        u32x2 vr;
+        u32x2 vv;
         if constexpr (KV8) {
-          vr = u32x2{Dt<DT>::fp8x2(vb8[buf][n], false), Dt<DT>::fp8x2(vb8[buf][n], true)};
+          const uint32_t codes = vb8[buf][n] & m8;  // a zero code is +0
+          vv = u32x2{Dt<DT>::fp8x2(codes, false), Dt<DT>::fp8x2(codes, true)};
         } else {
-          vr = vb[buf][n];
+          vv = u32x2{vb[buf][n].x & mlo, vb[buf][n].y & mhi};
         }
-        const u32x2 vv = {vr.x & mlo, vr.y & mhi};
         o[n] = Dt<DT>::mma16x16x16(vv, pb, o[n]);
       }
     };
@@ -537,7 +548,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     // blocks in flight already.
     if (prologue) {
 #pragma unroll
-      for (int q = 0; q < PF; ++q) issue(q, q);
+      for (int q = 0; q < PF; ++q) issue(q, q, pidn0);  // (never the next piece)
     }
 
     // The next piece: its item, query and first page ids load now, while
@@ -583,15 +594,21 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     // re-read the last block, an L2 hit, and compute it fully masked): with
     // no load under a branch the compiler's wait counts stay exact, so the
     // PF blocks in flight are never drained early.
-    // (n_pad >= NBUF: at least one step group, which the do-while tells the
-    // compiler, so no path reaches the hand-over without the waits below)
-    int64_t i0 = 0;
-    do {
+    //
+    // A step group's issues select their page-id window by value, the next
+    // piece's window 0 included.  Selecting pidn0 itself would make the
+    // compiler wait for that load (issued just before the first group) at the
+    // top of every group, draining the pipeline each time; the groups of a
+    // piece with two or more of them select pidn0_ready instead, which the end
+    // of each group refreshes (in the first group no issue reaches the next
+    // piece: its issues stop at block NBUF + PF - 1 < n_pad).  A piece of one
+    // group selects pidn0 and waits once.
+    auto step_group = [&](int64_t i0, uint32_t w_n0) {
       const uint32_t pid_ahead = load_window(c_seq, c_blk, wcur + 2);
 #pragma unroll
       for (int u = 0; u < NBUF; ++u) {
         const int64_t i = i0 + u;
-        issue(i + PF, (u + PF) % NBUF);
+        issue(i + PF, (u + PF) % NBUF, w_n0);
         compute(i, u);
       }
       // entered window wcur+1: move the windows up (at most NBUF + PF pages
@@ -604,20 +621,27 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       pid_later = pid_ahead;
       // The next piece's query and page ids must have arrived by the end of
       // the first step group (they are older than its loads): consume them
-      // here, where the wait count is exact, so the piece hand-over below
-      // does not wait on the loads in flight.
+      // here, where the wait count is exact, so neither the later groups nor
+      // the piece hand-over below wait on the loads in flight.
 #pragma unroll
       for (int kk = 0; kk < (kK32 ? KK : 1); ++kk) asm volatile("" ::"v"(qn4[kk]));
 #pragma unroll
       for (int kk = 0; kk < (kK32 ? 1 : KK); ++kk) asm volatile("" ::"v"(qn2[kk]));
-      asm volatile("" ::"v"(pidn0), "v"(pidn1));
-      i0 += NBUF;
-    } while (i0 < n_pad);
+      asm volatile("" ::"v"(pidn1));
+      asm volatile("v_mov_b32 %0, %1" : "=v"(pidn0_ready) : "v"(pidn0));
+    };
+    if (n_pad == NBUF) {
+      step_group(0, pidn0);
+    } else {
+      int64_t i0 = 0;
+      do {
+        step_group(i0, pidn0_ready);
+        i0 += NBUF;
+      } while (i0 < n_pad);
+    }
 
     // ---- finish the segment piece: exp-sum of head r16 over the 4 lane groups
-    float l = l_run;
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    const float l = sum_xor32(sum_xor16(l_run));
     if (r16 < hg) {
       const int64_t row = (il.row ? static_cast<int64_t>(il.row[c_s]) : c_s) * p.num_q_heads + qh_base + r16;
       if (complete) {
@@ -676,6 +700,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     for (int kk = 0; kk < (kK32 ? KK : 1); ++kk) qv4[kk] = qn4[kk];
 #pragma unroll
     for (int kk = 0; kk < (kK32 ? 1 : KK); ++kk) qv2[kk] = qn2[kk];
+    if constexpr (KV8) query_to_fp8<DT, KK>(qv4, q8);
     wcur = 0;
     pid_cur = pidn0;
     pid_nxt = pidn1;

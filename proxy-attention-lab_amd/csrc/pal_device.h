@@ -161,6 +161,98 @@ __device__ __forceinline__ u32x4 fp8x8_exact(u32x2 w) {
                Dt<DT>::fp8x2(w.y, true)};
 }
 
+// ---------------------------------------------------------------------------
+// fp8 e4m3 operands of the gfx950 scaled MFMA: D[16 x 16] += A[16 x 128]
+// B[128 x 16] with 32 codes per lane per operand.  Lane 16 g + i holds 32
+// k-slots of row i of A and the same 32 k-slots of column i of B (the two
+// operands distribute k alike, checked on the GPU against a host product),
+// so any assignment of dims to (lane group, byte) that A and B share gives
+// the inner product.  Output: lane l holds D[4 (l / 16) + e][l % 16], e < 4,
+// as in mma16x16x32.  sb is the E8M0 scale of B's column l % 16 (2^(sb -
+// 127)); A is unscaled.
+// ---------------------------------------------------------------------------
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mma_fp8_16x16x128(i32x8 a, i32x8 b, f32x4 c, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
+}
+
+// A query head as fp8 terms for mma_fp8_16x16x128.  With x = q 2^sh (sh per
+// head: the head's largest |q| scales into [128, 256)), the terms are hi =
+// e4m3(x), lo = e4m3(16 (x - hi)) and, for fp16 queries, lo2 = e4m3(16 (16
+// (x - hi) - lo)), each rounded to nearest even; term t carries the scale
+// 2^-(sh + 4 t).  Two terms are exact for bf16 (8 significant bits: hi keeps
+// 4, the remainder is k 2^(e - 7) with |k| <= 8) and three leave fp16 within
+// 2^-12 of each value, for every element above 2^-13 of the head's largest
+// (smaller ones are within 2^-21 of the largest).
+//
+// q4[kk]: the lane's 8 query values of k-step kk (16-bit, packed in pairs);
+// operand m takes the values of k-steps 4m .. 4m+3 as its bytes 0..31 (zeros
+// past KK).  The largest magnitude is taken over the 4 lane groups of the head.
+template <int DT, int KK>
+struct QueryFp8 {
+  static constexpr int kOps = (KK + 3) / 4;      // MFMAs per 128 dims
+  static constexpr int kTerms = DT == kBF16 ? 2 : 3;
+  i32x8 w[kTerms][kOps];
+  int s_hi;  // E8M0 scale of term 0; term t uses s_hi - 4 t
+};
+
+template <int DT, int KK>
+__device__ __forceinline__ void query_to_fp8(const u32x4 (&q4)[KK], QueryFp8<DT, KK>& out) {
+  constexpr int kOps = QueryFp8<DT, KK>::kOps;
+  constexpr int kTerms = QueryFp8<DT, KK>::kTerms;
+  // largest magnitude: for bf16 and fp16 alike the magnitude order of
+  // non-NaN values is the integer order of their low 15 bits
+  uint32_t mb = 0;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t w = q4[kk][c];
+      mb = max(mb, max(w & 0x7FFFu, (w >> 16) & 0x7FFFu));
+    }
+  }
+  mb = max(mb, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mb), 16, 64)));
+  mb = max(mb, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mb), 32, 64)));
+  // floor(log2 of the largest); zero and subnormal heads take the clamp
+  const int e = DT == kBF16 ? static_cast<int>(mb >> 7) - 127 : static_cast<int>(mb >> 10) - 15;
+  int sh = 7 - e;
+  sh = sh < -100 ? -100 : (sh > 119 ? 119 : sh);  // E8M0 scales stay in [0, 254]
+  const float mul = __uint_as_float(static_cast<uint32_t>(sh + 127) << 23);
+  out.s_hi = 127 - sh;
+#pragma unroll
+  for (int m = 0; m < kOps; ++m) {
+#pragma unroll
+    for (int wd = 0; wd < 8; ++wd) {  // word wd: values 4 wd .. 4 wd + 3 of operand m
+      const int kk = 4 * m + wd / 2;
+      float x[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (kk < KK) {
+          const uint32_t w = q4[kk][2 * (wd & 1) + t / 2];
+          x[t] = Dt<DT>::to_f32(static_cast<uint16_t>((t & 1) ? (w >> 16) : (w & 0xFFFFu))) * mul;
+        } else {
+          x[t] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int term = 0; term < kTerms; ++term) {
+        int code = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+        code = __builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], code, true);
+        out.w[term][m][wd] = code;
+        if (term + 1 < kTerms) {
+          const f32x2 b01 = __builtin_amdgcn_cvt_pk_f32_fp8(code, false);
+          const f32x2 b23 = __builtin_amdgcn_cvt_pk_f32_fp8(code, true);
+          x[0] = (x[0] - b01[0]) * 16.f;  // exact: the remainder of a rounding
+          x[1] = (x[1] - b01[1]) * 16.f;
+          x[2] = (x[2] - b23[0]) * 16.f;
+          x[3] = (x[3] - b23[1]) * 16.f;
+        }
+      }
+    }
+  }
+}
+
 // Eight fp8 e4m3 values (w: bytes 0..7) times scale s, as packed 16-bit
 // values of dtype DT (round to nearest even).
 template <int DT>
@@ -233,6 +325,18 @@ __device__ __forceinline__ float max_xor32(float v) {
 }
 __device__ __forceinline__ float sum_xor32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The same with lane l ^ 16 (v_permlane16_swap: the two results hold v of
+// lanes l and l ^ 16).
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  return m;
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
