@@ -153,6 +153,36 @@ __device__ __forceinline__ void rope_gptj(float (&x)[8], const float* cs, int f0
     x[2 * e + 1] = b * c + a * s;
   }
 }
+// Rotates the 4 values of a 16-byte piece (dims 4j..4j+3 of a head, j the
+// piece index) in place.  NeoX: w holds the partner piece's values (j xor
+// rot/8); GPT-J: the pairs sit inside the piece.  The products are those of
+// rope_neox / rope_gptj, rounded alike.
+__device__ __forceinline__ void rope_piece(float (&v)[4], const float (&w)[4], const float* cs, int j, int style,
+                                           int rot) {
+  const int half = rot / 2;
+  if (style == 1) {
+    const int pr = rot / 8;
+    if (j >= 2 * pr) return;  // past rotary_dim
+    const bool lo = j < pr;
+    const int d = 4 * (lo ? j : j - pr);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c = cs[d + e];
+      const float s = cs[half + d + e];
+      v[e] = lo ? v[e] * c - w[e] * s : v[e] * c + w[e] * s;
+    }
+  } else if (style == 2) {
+    if (4 * j >= rot) return;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float c = cs[2 * j + q];
+      const float s = cs[half + 2 * j + q];
+      const float a = v[2 * q], b = v[2 * q + 1];
+      v[2 * q] = a * c - b * s;
+      v[2 * q + 1] = b * c + a * s;
+    }
+  }
+}
 #pragma clang fp contract(on)
 
 // Stores chunk c (dims 8c..8c+7) of a token at `slot` of the K block that
@@ -274,6 +304,63 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
     // ---- queries: rotate and cast head qh of the window's rows (a row is
     // contiguous in and out, so units run fastest: whole lines per wave)
     const int qh = blockIdx.y - p.num_kv_heads;
+    if constexpr (SRC == kF32) {
+      // fp32 rows of head dims 32/64/128/256: 16-byte pieces, lane j of a
+      // token's hd/4 lanes holding dims 4j..4j+3, so every load and store
+      // instruction covers whole lines (8-value units store 16 bytes 32 bytes
+      // apart: 1.48x the written bytes), with non-temporal loads and stores
+      // (the rows pass once; kept in L2 they pushed out the cos/sin table,
+      // which every head re-reads: 1.33x the read bytes)
+      const int rot = p.rotary_dim;
+      const bool hd_ok = hd == 32 || hd == 64 || hd == 128 || hd == 256;
+      const bool rot_ok = p.rope_style != 1 || (rot >= 8 && rot <= hd && (rot & (rot - 1)) == 0);
+      if (hd_ok && rot_ok) {
+        constexpr int kPieces = (WIN * 32 + kThreads - 1) / kThreads;  // per thread per round (hd <= 128)
+        const int lpt = hd / 4;  // pieces of a row; divides the wavefront
+        const int n_items = nwin * lpt;
+        const int64_t q_row = static_cast<int64_t>(p.num_q_heads) * hd;
+#pragma unroll 1
+        for (int base = 0; base < n_items; base += kPieces * kThreads) {  // two rounds at hd 256
+          f32x4 xq[kPieces];
+          int pos[kPieces];
+#pragma unroll
+          for (int k = 0; k < kPieces; ++k) {
+            const int it = base + tid + k * kThreads;
+            xq[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            pos[k] = -1;
+            if (it < n_items) {
+              const int i = it / lpt;
+              xq[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
+                  static_cast<const float*>(p.q_in) + (t0 + i) * q_row + static_cast<int64_t>(qh) * hd + 4 * (it % lpt)));
+              pos[k] = p.write_pos[t0 + i];
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < kPieces; ++k) {
+            const int it = base + tid + k * kThreads;
+            float v[4] = {xq[k][0], xq[k][1], xq[k][2], xq[k][3]};
+            float w[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.rope_style == 1) {  // every lane takes part (a token's lanes are valid together)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w[e] = __shfl_xor(v[e], rot / 8, kWave);
+            }
+            if (it < n_items) {
+              const int i = it / lpt;
+              const int j = it % lpt;
+              if (p.rope_style != 0 && pos[k] >= 0 && pos[k] < p.cos_sin_rows)
+                rope_piece(v, w, p.cos_sin + static_cast<int64_t>(pos[k]) * rot, j, p.rope_style, rot);
+              const u32x2 packed = p.q_out_dtype == kBF16
+                                       ? u32x2{Dt<kBF16>::pack2(v[0], v[1]), Dt<kBF16>::pack2(v[2], v[3])}
+                                       : u32x2{Dt<kF16>::pack2(v[0], v[1]), Dt<kF16>::pack2(v[2], v[3])};
+              __builtin_nontemporal_store(packed, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.q_out) +
+                                                                         (t0 + i) * q_row +
+                                                                         static_cast<int64_t>(qh) * hd + 4 * j));
+            }
+          }
+        }
+        return;
+      }
+    }
     const int64_t q_row = static_cast<int64_t>(p.num_q_heads) * hd;
     Raw8<SRC> rx[kItems], ry[kItems];
     int pos[kItems];
