@@ -460,7 +460,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       }
     };
 
-    float m_run = -INFINITY;  // running max (raw score units) of head r16
+    float m_run = -INFINITY;  // running max of head r16, in log2 units (score * scale_log2)
     float l_run = 0.f;        // this lane's share of the exp-sum of head r16
     f32x4 o[NT];
 #pragma unroll
@@ -483,7 +483,6 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #pragma unroll
           for (int t = 0; t < q8.kTerms; ++t) acc = mma_fp8_16x16x128(a, q8.w[t][m], acc, q8.s_hi - 4 * t);
         }
-        acc *= bks[buf];  // the block's K scale
       } else {
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
@@ -494,6 +493,12 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
           }
         }
       }
+      // scores in log2 units (fp8: with the block's K scale in the same
+      // multiply), so each exponent below is score - max: exactly 0 for the
+      // max key whatever the scores' size (an fma of score * scale_log2
+      // against a rounded max * scale_log2 leaves that product's rounding
+      // error, which overflows exp2 once scores pass ~2^31)
+      acc *= KV8 ? bks[buf] * p.scale_log2 : p.scale_log2;
       // tokens past the end (and whole invalid blocks) are masked: token
       // 4g + e of the block is a key when e < kl (the block's key count is
       // uniform, so the 64-bit part is scalar)
@@ -508,10 +513,10 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       }
       bm = max_xor32(max_xor16(bm));  // over the 4 lane groups (scores are finite or -inf)
       const float m_new = fmaxf(m_run, bm);
-      const float msc = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
+      const float mref = (m_new == -INFINITY) ? 0.f : m_new;  // a head with no key yet: every exponent is -inf
       if (__ballot(m_new > m_run && m_run != -INFINITY)) {
         // the max of some head grew: rescale the running state
-        const float alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(fmaf(m_run, p.scale_log2, -msc));
+        const float alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mref);
         l_run *= alpha;
 #pragma unroll
         for (int n = 0; n < NT; ++n) o[n] *= alpha;
@@ -520,7 +525,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       float pe[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pe[e] = __builtin_amdgcn_exp2f(fmaf(sc4[e], p.scale_log2, -msc));
+        pe[e] = __builtin_amdgcn_exp2f(sc4[e] - mref);
         l_run += pe[e];
       }
       // fp8: the block's V scale rides on the probabilities (the exp-sum stays unscaled)
@@ -663,7 +668,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
           *reinterpret_cast<u32x2*>(p.part_o + slot * HD + 16 * n + 4 * g) = pk;
         }
         if (g == 0) {
-          const f32x2 ml = {(m_run == -INFINITY) ? -INFINITY : m_run * p.scale_log2, l};
+          const f32x2 ml = {m_run, l};  // the max is in log2 units already
           *reinterpret_cast<f32x2*>(p.part_ml + slot * 2) = ml;
         }
       }
@@ -1566,8 +1571,11 @@ hipError_t decode_resident_workers(int dtype, int head_dim, int tokens_per_page,
     int groups_per_cu = 0;
     err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&groups_per_cu, fn, kGroupThreads, 0);
     if (err != hipSuccess) return err;
-    if (groups_per_cu < 1) groups_per_cu = 1;
-    res = cus * groups_per_cu * kWorkersPerGroup;
+    if (groups_per_cu < 1) return hipErrorInvalidConfiguration;  // the kernel does not fit a CU
+    // One workgroup per CU (one wavefront per SIMD, PF blocks in flight
+    // each), whatever else the registers would allow: a second workgroup per
+    // CU measured slower and doubles the split segments to merge.
+    res = cus * kWorkersPerGroup;
   }
   {
     std::lock_guard<std::mutex> lock(mu);

@@ -217,7 +217,10 @@ __device__ __forceinline__ void query_to_fp8(const u32x4 (&q4)[KK], QueryFp8<DT,
   // floor(log2 of the largest); zero and subnormal heads take the clamp
   const int e = DT == kBF16 ? static_cast<int>(mb >> 7) - 127 : static_cast<int>(mb >> 10) - 15;
   int sh = 7 - e;
-  sh = sh < -100 ? -100 : (sh > 119 ? 119 : sh);  // E8M0 scales stay in [0, 254]
+  // E8M0 scales 127 - sh - 4 t stay in [0, 254] and 2^sh is a normal float;
+  // -126 covers every finite bf16 and fp16 head (their largest exponent is
+  // 127), 119 only heads below 2^-112, whose scores vanish anyway
+  sh = sh < -126 ? -126 : (sh > 119 ? 119 : sh);
   const float mul = __uint_as_float(static_cast<uint32_t>(sh + 127) << 23);
   out.s_hi = 127 - sh;
 #pragma unroll

@@ -26,6 +26,33 @@ def randn_bits(rng: np.random.Generator, shape, dtype: str, scale: float = 1.0) 
     return orc.f32_to_bits(x, dtype)
 
 
+def extreme_query_bits(rng: np.random.Generator, shape, dtype: str, tiles: bool = False) -> np.ndarray:
+    """Queries [..., H >= 5, HD] whose first five heads span the dtype's
+    range: zeros; tiny values (fp16: subnormals); huge values; a head with
+    half its dims large and half small; values near the bottom of bf16's
+    normal range, or near the fp16 maximum.  The other heads are N(0, 1).
+
+    Decode takes its exponents as exp2(score - max) in log2 units, exact at
+    any size, so the huge heads there reach scores past 2^31 (one-hot
+    softmax).  The prefill tiles take one fma against the rounded max, exact
+    while the scaled max stays below ~2^14; with tiles=True the large heads
+    are held to magnitude 1e3 (scaled scores of a few thousand)."""
+    x = rng.standard_normal(size=shape, dtype=np.float32)
+    bf = dtype == "bf16"
+    half = shape[-1] // 2
+    big = 1e3 if tiles else (1e20 if bf else 3e3)
+    x[..., 0, :] = 0.0
+    x[..., 1, :] *= np.float32(1e-30 if bf else 1e-7)
+    x[..., 2, :] *= np.float32(big)
+    x[..., 3, :half] *= np.float32(1e3 if tiles else (1e6 if bf else 1e2))
+    x[..., 3, half:] *= np.float32(1e-3 if tiles else (1e-6 if bf else 1e-2))
+    if bf:
+        x[..., 4, :] *= np.float32(1e-38)
+    else:
+        x[..., 4, :] = np.clip(x[..., 4, :] * (1e3 if tiles else 3e4), -65000, 65000)
+    return orc.f32_to_bits(x, dtype)
+
+
 @dataclass
 class PagedCase:
     dtype: str

@@ -14,7 +14,7 @@ import kat_cases
 import proxy_attention_lab as pal
 from gpu_util import announce, dev_bits, dev_index, host_bits, host_f32
 from oracle import pal_oracle as orc
-from pal_cases import assert_close, compact_subset, make_paged_case, randn_bits
+from pal_cases import assert_close, compact_subset, extreme_query_bits, make_paged_case, randn_bits
 
 pytestmark = pytest.mark.gpu
 DTYPES = ["f16", "bf16"]
@@ -198,3 +198,16 @@ def test_decode_many_pieces_per_worker():
     case = make_paged_case(16, lens, 32, 8, 128, 16, "bf16", garbage_tail=True)
     q = randn_bits(rng, (900, 32, 128), "bf16")
     _check(case, q, what="900 sequences")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("partition", [0, 512])
+def test_decode_query_magnitudes(dtype, partition):
+    """Query heads across the dtype's range (zeros, tiny, huge, mixed,
+    near the range ends): the softmax takes exp2(score - max) in log2 units,
+    so even scores past 2^31 stay finite and match the oracle."""
+    lens = [1, 17, 300, 1000, 2049]
+    case = make_paged_case(72 + partition, lens, 16, 4, 128, 16, dtype)
+    q = extreme_query_bits(np.random.default_rng(72), (len(lens), 16, 128), dtype)
+    out = _check(case, q, partition, f"query magnitudes p{partition}")
+    assert np.isfinite(host_f32(out)).all()

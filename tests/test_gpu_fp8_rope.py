@@ -17,7 +17,7 @@ import torch
 import proxy_attention_lab as pal
 from gpu_util import DEV, announce, dev_bits, dev_index, host_bits, host_f32
 from oracle import pal_oracle as orc
-from pal_cases import assert_close, compact_subset, make_paged_case, randn_bits
+from pal_cases import assert_close, compact_subset, extreme_query_bits, make_paged_case, randn_bits
 
 pytestmark = pytest.mark.gpu
 TD = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
@@ -220,6 +220,24 @@ def test_decode_fp8_pages(dtype, hd, tpp, partition):
     out = _decode_fp8(case, q, kc, vc, ks, vs, partition)
     ref = orc.paged_attention_decode(q, kc, vc, case.page_table, case.seq_lens, dtype, kv_scales=(ks, vs))
     assert_close(out, ref, dtype, f"fp8 decode {dtype} hd{hd} tpp{tpp} p{partition}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("partition", [0, 512])
+def test_decode_fp8_query_magnitudes(dtype, partition):
+    """The fp8 decode turns each query head into fp8 terms scaled by a
+    per-head power of two: heads across the dtype's range (extreme_query_bits)
+    attend as the oracle does."""
+    lens = [1, 17, 300, 1000, 2049]
+    rng = np.random.default_rng(71 + partition)
+    case = make_paged_case(71, lens, 16, 4, 128, 16, dtype)
+    kc, vc, ks, vs = fp8_case(case, rng)
+    q = extreme_query_bits(rng, (len(lens), 16, 128), dtype)
+    announce(f"decode fp8 query magnitudes {dtype} partition={partition}")
+    out = _decode_fp8(case, q, kc, vc, ks, vs, partition)
+    ref = orc.paged_attention_decode(q, kc, vc, case.page_table, case.seq_lens, dtype, kv_scales=(ks, vs))
+    assert np.isfinite(out).all()
+    assert_close(out, ref, dtype, f"fp8 decode query magnitudes {dtype} p{partition}")
 
 
 def test_decode_fp8_config2_shape_subset():

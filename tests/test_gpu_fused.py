@@ -15,7 +15,7 @@ import torch
 import proxy_attention_lab as pal
 from gpu_util import announce, dev_bits, dev_index, host_bits, host_f32
 from oracle import pal_oracle as orc
-from pal_cases import assert_close, make_fused_case, make_paged_case, make_prefill_case, randn_bits
+from pal_cases import assert_close, extreme_query_bits, make_fused_case, make_paged_case, make_prefill_case, randn_bits
 
 pytestmark = pytest.mark.gpu
 DTYPES = ["f16", "bf16"]
@@ -175,3 +175,14 @@ def test_fused_long_history_window(tpp):
     fc = make_fused_case(70 + tpp, [100, 30000], [(26000 if tpp == 16 else 38000, 64), (9000, 40)], 32, 8, 128,
                          tpp, "bf16", block=64)
     _check_fused(fc, f"long history window tpp{tpp}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fused_query_magnitudes(dtype):
+    """A mixed batch whose query heads span the dtype's range (zeros, tiny,
+    large, mixed, near the range ends), in its decode rows and its tiles
+    (the large heads held to the tiles' exact range)."""
+    fc = make_fused_case(74, [5, 300, 1200], [(0, 70), (200, 130)], 16, 4, 128, 16, dtype)
+    fc.queries = extreme_query_bits(np.random.default_rng(74), fc.queries.shape, dtype, tiles=True)
+    out = _check_fused(fc, f"query magnitudes {dtype}")
+    assert np.isfinite(out).all()

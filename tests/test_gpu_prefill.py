@@ -15,7 +15,7 @@ import kat_cases
 import proxy_attention_lab as pal
 from gpu_util import announce, dev_bits, dev_index, host_bits, host_f32
 from oracle import pal_oracle as orc
-from pal_cases import assert_close, make_prefill_case, sdpa_prefill_case
+from pal_cases import assert_close, extreme_query_bits, make_prefill_case, sdpa_prefill_case
 
 pytestmark = pytest.mark.gpu
 DTYPES = ["f16", "bf16"]
@@ -151,3 +151,17 @@ def test_prefill_runtime_page_sizes(tpp, dtype):
 def test_prefill_runtime_page_size_head_dims(hd):
     _check(hd + 1, [5, 40, 0, 129], 45, 8, 2, hd, 8, "bf16", f"tpp8 hd{hd}")
     _check(hd + 2, [5, 40, 0, 129], 45, 8, 2, hd, 64, "f16", f"tpp64 hd{hd}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_prefill_query_magnitudes(dtype):
+    """Query heads across the dtype's range (zeros, tiny, large, mixed, near
+    the range ends) through the tile path, the large heads held to the
+    tiles' exact range (extreme_query_bits with tiles=True)."""
+    case, q, k, v = make_prefill_case(73, [0, 40, 300], 70, 16, 4, 128, 16, dtype)
+    q = extreme_query_bits(np.random.default_rng(73), q.shape, dtype, tiles=True)
+    announce(f"prefill query magnitudes {dtype}")
+    out = host_f32(_prefill_gpu(q, k, v, case.k_pool, case.v_pool, case.page_table, case.seq_lens, dtype))
+    assert np.isfinite(out).all()
+    ref = orc.paged_attention_prefill(q, k, v, case.k_pool, case.v_pool, case.page_table, case.seq_lens, dtype)
+    assert_close(out, ref, dtype, f"prefill query magnitudes {dtype}")
