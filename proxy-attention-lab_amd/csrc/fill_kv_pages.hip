@@ -183,6 +183,39 @@ __device__ __forceinline__ void rope_piece(float (&v)[4], const float (&w)[4], c
     }
   }
 }
+// Rotates a pair of 16-byte pieces of one K row in place: x holds dims
+// 4j..4j+3, y dims hd/2 + 4j .. +3.  NeoX (rotary_dim == hd): the two are
+// each other's partners; GPT-J: the pairs sit inside each piece.  The
+// products are those of rope_neox / rope_gptj, rounded alike.
+__device__ __forceinline__ void rope_piece_pair(float (&x)[4], float (&y)[4], const float* cs, int j, int style,
+                                                int rot, int hd) {
+  const int half = rot / 2;
+  if (style == 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c = cs[4 * j + e];
+      const float s = cs[half + 4 * j + e];
+      const float a = x[e], b = y[e];
+      x[e] = a * c - b * s;
+      y[e] = b * c + a * s;
+    }
+  } else if (style == 2) {
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+      float(&v)[4] = side ? y : x;
+      const int d0 = (side ? hd / 2 : 0) + 4 * j;
+      if (d0 >= rot) continue;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float c = cs[d0 / 2 + q];
+        const float s = cs[half + d0 / 2 + q];
+        const float a = v[2 * q], b = v[2 * q + 1];
+        v[2 * q] = a * c - b * s;
+        v[2 * q + 1] = b * c + a * s;
+      }
+    }
+  }
+}
 #pragma clang fp contract(on)
 
 // Stores chunk c (dims 8c..8c+7) of a token at `slot` of the K block that
@@ -410,11 +443,40 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
   const int lrow = krow_bytes + kRowPad;                             // its LDS row stride
   uint8_t* k_lds = dyn_lds;
   uint8_t* v_lds = dyn_lds + WIN * lrow;
-  // ---- issue every source load of this thread: K units and V chunks of the
-  // window's rows (units / chunks fastest, so a wavefront reads whole lines)
+  // fp32 rows into 16-bit pools (the RoPE fill's usual case): lane j of a
+  // token's hd/8 lanes takes the 16-byte pieces j and j + hd/8, i.e. dims
+  // 4j..4j+3 of either half of the row, so each load instruction covers
+  // whole lines and reads them non-temporally (8-value units read two 16-byte
+  // halves 32 bytes apart per instruction: 1.26 x the read bytes), and a
+  // NeoX rotation over the whole head pairs the lane's own two pieces
+  constexpr bool kPieceSrc = SRC == kF32 && DST != kFP8;
+  const bool piece_path = kPieceSrc && (p.rope_style != 1 || p.rotary_dim == hd);
+  f32x4 pk[kPieceSrc ? kItems : 1][2], pv[kPieceSrc ? kItems : 1][2];
+  if constexpr (kPieceSrc) {
+    if (piece_path) {
+#pragma unroll
+      for (int k = 0; k < kItems; ++k) {
+        const int it = tid + k * kThreads;
+        const int i = it / chunks;  // hd/8 lanes per token
+        if (i < nwin) {
+          const int64_t row = (t0 + i) * k_row + static_cast<int64_t>(h) * hd + 4 * (it % chunks);
+#pragma unroll
+          for (int sd = 0; sd < 2; ++sd) {
+            pk[k][sd] = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4*>(static_cast<const float*>(p.new_k) + row + sd * (hd / 2)));
+            pv[k][sd] = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4*>(static_cast<const float*>(p.new_v) + row + sd * (hd / 2)));
+          }
+        }
+      }
+    }
+  }
+  // ---- otherwise issue every source load of this thread: K units and V
+  // chunks of the window's rows (units / chunks fastest, so a wavefront
+  // reads whole lines of 16-bit rows)
   Raw8<SRC> kx[kItems], ky[kItems], vx[kItems];
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) {
+  for (int k = 0; k < kItems && !piece_path; ++k) {
     const int it = tid + k * kThreads;
     const int i = it / units;
     if (i < nwin) {
@@ -487,8 +549,47 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
 
   const int64_t head_block = static_cast<int64_t>(hd) * tpp * EB;  // bytes per (page, kv head) block
   // ---- single tokens to the pool, run tokens into LDS
+  if constexpr (kPieceSrc) {
+    if (piece_path) {
 #pragma unroll
-  for (int k = 0; k < kItems; ++k) {
+      for (int k = 0; k < kItems; ++k) {
+        const int it = tid + k * kThreads;
+        const int i = it / chunks;
+        const int j = it % chunks;
+        if (i >= nwin || slot_lds[i] < 0) continue;
+        float x[2][4];
+#pragma unroll
+        for (int sd = 0; sd < 2; ++sd)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[sd][e] = pk[k][sd][e];
+        if (p.rope_style != 0)
+          rope_piece_pair(x[0], x[1], p.cos_sin + static_cast<int64_t>(pos_lds[i]) * p.rotary_dim, j, p.rope_style,
+                          p.rotary_dim, hd);
+        const bool single = kind_lds[i] == 1;
+        const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
+#pragma unroll
+        for (int sd = 0; sd < 2; ++sd) {
+          const int d0 = sd * (hd / 2) + 4 * j;  // first dim of the piece
+          const u32x2 kw = {Dt<DST>::pack2(x[sd][0], x[sd][1]), Dt<DST>::pack2(x[sd][2], x[sd][3])};
+          const u32x2 vw = {Dt<DST>::pack2(pv[k][sd][0], pv[k][sd][1]), Dt<DST>::pack2(pv[k][sd][2], pv[k][sd][3])};
+          if (single) {
+            // K: half of stripe d0 / 8; V: one 2-byte value per row
+            *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.k_pool) + hb +
+                                      (static_cast<int64_t>(d0 >> 3) * tpp + slot_lds[i]) * 16 + (d0 & 4) * 2) = kw;
+            uint8_t* col = static_cast<uint8_t*>(p.v_pool) + hb + (static_cast<int64_t>(d0) * tpp + slot_lds[i]) * 2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              *reinterpret_cast<uint16_t*>(col + e * tpp * 2) = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+          } else {  // a run token: its rows into LDS as they are
+            *reinterpret_cast<u32x2*>(k_lds + i * lrow + d0 * 2) = kw;
+            *reinterpret_cast<u32x2*>(v_lds + i * lrow + d0 * 2) = vw;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kItems && !piece_path; ++k) {
     const int it = tid + k * kThreads;
     {  // K unit
       const int i = it / units;
