@@ -152,6 +152,35 @@ def test_rope_fill_bit_exact(style, rot, src, kv):
     assert np.array_equal(host_bits(qo), eq), "rotated queries differ"
 
 
+@pytest.mark.parametrize("hd", [32, 64, 96, 256])
+@pytest.mark.parametrize("style,rot_frac", [("neox", 1), ("gptj", 2)])
+def test_rope_fill_head_dims(hd, style, rot_frac):
+    """fp32 rows into bf16 pools at other head dims: the query rows and the
+    K/V rows move in 16-byte pieces (lanes per token hd/4 and hd/8, a token
+    straddling wavefronts at HD 96), NeoX over the whole head, GPT-J over half
+    of it; pools and rotated queries bit-exact."""
+    hkv, hq, tpp = 2, 8, 16
+    rot = hd // rot_frac
+    k, v, pt, pos, q2s, _ = fill_layout(hd + rot_frac, hkv, hd, tpp, "bf16")
+    rng = np.random.default_rng(hd * 10 + rot_frac)
+    n = len(pos)
+    nk = src_values(rng, (n, hkv, hd), "f32", 2.0)
+    nv = src_values(rng, (n, hkv, hd), "f32", 2.0)
+    q = src_values(rng, (n, hq, hd), "f32", 2.0)
+    table = pal.rope_cos_sin_cache(512, rot, 10000.0, device=DEV)
+    announce(f"rope fill head dim {hd} {style} rot={rot}")
+    kd, vd = dev_pool(k, "bf16"), dev_pool(v, "bf16")
+    _, _, qo = pal.rope_fill_kv_pages(dev_f32(nk, "f32"), dev_f32(nv, "f32"), kd, vd, dev_index(pt, torch.uint32),
+                                      dev_index(pos), dev_index(q2s, torch.uint32), table, queries=dev_f32(q, "f32"),
+                                      rotary_dim=rot, style=style, query_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    ek, ev, eq = orc.fill_kv_pages_ex(nk, nv, k, v, "bf16", pt, pos, q2s, rope=(table.cpu().numpy(), rot, style),
+                                      queries=q, q_out_dtype="bf16")
+    assert np.array_equal(host_pool(kd, "bf16"), ek), "K pool differs"
+    assert np.array_equal(host_pool(vd, "bf16"), ev), "V pool differs"
+    assert np.array_equal(host_bits(qo), eq), "rotated queries differ"
+
+
 def test_rope_fill_positions_outside_table():
     """Tokens whose position has no row in the cos/sin table leave the pools
     alone; their queries come back cast, unrotated."""
