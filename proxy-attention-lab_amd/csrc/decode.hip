@@ -1386,7 +1386,17 @@ hipError_t launch_merge(const DecodeParams& p, hipStream_t stream) {
     const int64_t segments = p.num_seqs * p.num_kv_heads * p.head_chunks;
     constexpr int64_t slices = (HD + kSegDims - 1) / (HD < kSegDims ? HD : kSegDims);
     const int64_t units = segments * p.hg_max * slices;
-    if ((p.tokens_per_worker > 0 || segments * 4 <= p.num_workers) && units > 0 && units <= kMaxSegMergeGroups) {
+    // The segment merge pays one workgroup per (segment, head, dim slice),
+    // worth it once a segment has many contributors (its 64 contributor lanes
+    // busy); otherwise the slot merge is faster (config 2 in partition-512
+    // mode: 142 -> 116 us with the slot merge; 8 seqs of 32-128K in equal
+    // shares, 16 per segment: the same; 4 seqs, 32 per segment: the segment
+    // merge 1 us faster).  Fixed chunks: the most contributors a sequence can
+    // have (page-table capacity / partition size); equal shares: the average.
+    const int64_t contrib = p.tokens_per_worker > 0
+                                ? (p.page_table_width * TPP + p.tokens_per_worker - 1) / p.tokens_per_worker
+                                : p.num_workers / (segments > 0 ? segments : 1);
+    if (contrib >= (p.tokens_per_worker > 0 ? 64 : 32) && units > 0 && units <= kMaxSegMergeGroups) {
       hipLaunchKernelGGL((decode_merge_seg_kernel<DT, HD, TPP>), dim3(static_cast<unsigned>(units)),
                          dim3(kGroupThreads), 0, stream, p);
       return hipGetLastError();
