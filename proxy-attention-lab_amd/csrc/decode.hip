@@ -367,7 +367,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   u32x4 kb4[NBUF][KV8 ? KL8 : (kK32 ? KK : 1)];
   u32x2 kb2[NBUF][kK32 ? 1 : KK];
   u32x2 vb[NBUF][KV8 ? 1 : NT];
-  uint32_t vb8[NBUF][KV8 ? NT : 1];
+  u32x4 vq8[NBUF][KV8 ? NT / 4 : 1];
   float bks[NBUF], bvs[NBUF];  // fp8: the block's (page, kv head) scales
   bool bv[NBUF];
 
@@ -438,9 +438,13 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
           const int c = g + 4 * j;  // stripe of dims 16c .. 16c+15
           kb4[buf][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
         }
+        // V: lane 16g + i reads the block's 16 codes of dim row 64q + 16g + i
+        // (one 16-byte load per 64 rows instead of four 4-byte ones); compute
+        // transposes them across the lane groups
+        const uint8_t* vrow = (to_next ? vb_x : vbase) + static_cast<int64_t>(page) * page_stride + slot0;
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
-          vb8[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vp + (16 * n + r16) * TPP));
+        for (int q = 0; q < NT / 4; ++q)
+          vq8[buf][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow + (64 * q + 16 * g + r16) * TPP));
       } else {
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
@@ -536,11 +540,17 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       const uint32_t mlo = (kl > 0 ? 0x0000FFFFu : 0u) | (kl > 1 ? 0xFFFF0000u : 0u);
       const uint32_t mhi = (kl > 2 ? 0x0000FFFFu : 0u) | (kl > 3 ? 0xFFFF0000u : 0u);
       const uint32_t m8 = kl >= 4 ? 0xFFFFFFFFu : (kl <= 0 ? 0u : (0xFFFFFFFFu >> (32 - 8 * kl)));
+      // fp8: lane (g, i) gets codes of tokens 4g .. 4g+3 of dim rows 16n + i
+      u32x4 vt[KV8 ? NT / 4 : 1];
+      if constexpr (KV8) {
+#pragma unroll
+        for (int q = 0; q < NT / 4; ++q) vt[q] = transpose_lane_groups4(vq8[buf][q]);
+      }
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
         u32x2 vv;
         if constexpr (KV8) {
-          const uint32_t codes = vb8[buf][n] & m8;  // a zero code is +0
+          const uint32_t codes = vt[n >> 2][n & 3] & m8;  // a zero code is +0
           vv = u32x2{Dt<DT>::fp8x2(codes, false), Dt<DT>::fp8x2(codes, true)};
         } else {
           vv = u32x2{vb[buf][n].x & mlo, vb[buf][n].y & mhi};

@@ -343,6 +343,23 @@ __device__ __forceinline__ float sum_xor16(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// 4 x 4 transpose of 32-bit words across the four 16-lane groups: lane
+// 16 g + i holds words 0..3 of "row" g (of its column i) and receives word g
+// of rows 0..3.  v_permlane32_swap exchanges the upper 32 lanes of its first
+// operand with the lower 32 of its second, v_permlane16_swap the odd 16-lane
+// rows of its first operand with the even rows of its second (each returns
+// both operands).  After the two 32-lane swaps groups 0, 1 hold words 0, 1
+// of rows g (x02[0], x13[0]) and g + 2 (x02[1], x13[1]), groups 2, 3 words
+// 2, 3 of rows g - 2 and g; the 16-lane swaps then leave word g of rows 0, 1
+// in y and of rows 2, 3 in z.
+__device__ __forceinline__ u32x4 transpose_lane_groups4(u32x4 w) {
+  const auto x02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  const auto x13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  const auto y = __builtin_amdgcn_permlane16_swap(x02[0], x13[0], false, false);
+  const auto z = __builtin_amdgcn_permlane16_swap(x02[1], x13[1], false, false);
+  return u32x4{y[0], y[1], z[0], z[1]};
+}
+
 // Index of this thread's wavefront, forced into a scalar register so that
 // addresses derived from it stay uniform (scalar loads of page-table entries).
 __device__ __forceinline__ int wave_id() {
