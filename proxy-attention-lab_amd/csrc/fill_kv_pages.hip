@@ -129,34 +129,35 @@ struct Store8<kFP8> {
 template <int DST>
 constexpr int elem_bytes() { return DST == kFP8 ? 1 : 2; }
 
-// Rotates the 8 values of chunk `lo` (dims d0..d0+7) with their partners:
-// NeoX: chunk `hi` holds dims d0 + rot/2 ..; GPT-J: pairs inside the chunk.
-// cs: the position's row of the cos/sin table.
+// Rotates the 8 values of chunk x (dims d0..d0+7) in place.  NeoX: y holds
+// their partners (dims d0 + rot/2 ..) and is rotated too; GPT-J: the pairs
+// sit inside the chunk.  cs: the position's row of the cos/sin table, f0 the
+// chunk's first table index (NeoX d0, GPT-J d0 / 2).  Both styles run one
+// unrolled body whose operands are selected by value: with a branch per
+// style the compiler merged the two styles' stores behind a run-time address
+// and put x and y on the stack.
 #pragma clang fp contract(off)
-__device__ __forceinline__ void rope_neox(float (&lo)[8], float (&hi)[8], const float* cs, int f0, int half) {
+__device__ __forceinline__ void rope_unit(float (&x)[8], float (&y)[8], const float* cs, int f0, int half, bool neox) {
+  float xo[8], yo[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float c = cs[f0 + e];
-    const float s = cs[half + f0 + e];
-    const float a = lo[e], b = hi[e];
-    lo[e] = a * c - b * s;
-    hi[e] = b * c + a * s;
+    const int f = f0 + (neox ? e : e >> 1);
+    const float c = cs[f];
+    const float s = cs[half + f];
+    const float t = (neox ? y[e] : x[e ^ 1]) * s;
+    xo[e] = x[e] * c + ((neox || (e & 1) == 0) ? -t : t);  // a c - b s, or b c + a s
+    yo[e] = y[e] * c + x[e] * s;
   }
-}
-__device__ __forceinline__ void rope_gptj(float (&x)[8], const float* cs, int f0, int half) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float c = cs[f0 + e];
-    const float s = cs[half + f0 + e];
-    const float a = x[2 * e], b = x[2 * e + 1];
-    x[2 * e] = a * c - b * s;
-    x[2 * e + 1] = b * c + a * s;
+  for (int e = 0; e < 8; ++e) {
+    x[e] = xo[e];
+    y[e] = neox ? yo[e] : y[e];
   }
 }
 // Rotates the 4 values of a 16-byte piece (dims 4j..4j+3 of a head, j the
 // piece index) in place.  NeoX: w holds the partner piece's values (j xor
 // rot/8); GPT-J: the pairs sit inside the piece.  The products are those of
-// rope_neox / rope_gptj, rounded alike.
+// rope_unit, rounded alike.
 __device__ __forceinline__ void rope_piece(float (&v)[4], const float (&w)[4], const float* cs, int j, int style,
                                            int rot) {
   const int half = rot / 2;
@@ -186,7 +187,7 @@ __device__ __forceinline__ void rope_piece(float (&v)[4], const float (&w)[4], c
 // Rotates a pair of 16-byte pieces of one K row in place: x holds dims
 // 4j..4j+3, y dims hd/2 + 4j .. +3.  NeoX (rotary_dim == hd): the two are
 // each other's partners; GPT-J: the pairs sit inside each piece.  The
-// products are those of rope_neox / rope_gptj, rounded alike.
+// products are those of rope_unit, rounded alike.
 __device__ __forceinline__ void rope_piece_pair(float (&x)[4], float (&y)[4], const float* cs, int j, int style,
                                                 int rot, int hd) {
   const int half = rot / 2;
@@ -269,11 +270,12 @@ struct Raw8<kF32> {
 // K work unit u of a row: NeoX rotation pairs chunk c with c + rot/16, so
 // unit u < rot/16 is that pair; every other unit is one chunk.  Without
 // NeoX pairs every unit is one chunk.
-__device__ __forceinline__ int k_units(const FillParams& p) {
-  return p.rope_style == 1 ? p.head_dim / 8 - p.rotary_dim / 16 : p.head_dim / 8;
+// (style: the call's rope style, 0 in the kernels compiled without RoPE)
+__device__ __forceinline__ int k_units(const FillParams& p, int style) {
+  return style == 1 ? p.head_dim / 8 - p.rotary_dim / 16 : p.head_dim / 8;
 }
-__device__ __forceinline__ void unit_chunks(const FillParams& p, int u, int& c0, int& c1) {
-  if (p.rope_style == 1) {
+__device__ __forceinline__ void unit_chunks(const FillParams& p, int style, int u, int& c0, int& c1) {
+  if (style == 1) {
     const int pairs = p.rotary_dim / 16;
     if (u < pairs) {
       c0 = u;
@@ -290,16 +292,13 @@ __device__ __forceinline__ void unit_chunks(const FillParams& p, int u, int& c0,
 
 // Rotates the unit's chunk(s) in place (x: chunk c0, y: chunk c1 of a NeoX
 // pair) with row `pos` of the table, when rotate.
-__device__ __forceinline__ void rotate_unit(const FillParams& p, int c0, int c1, int pos, bool rotate, float (&x)[8],
-                                            float (&y)[8]) {
-  if (!rotate || p.rope_style == 0 || 8 * c0 >= p.rotary_dim) return;
+__device__ __forceinline__ void rotate_unit(const FillParams& p, int style, int c0, int c1, int pos, bool rotate,
+                                            float (&x)[8], float (&y)[8]) {
+  if (!rotate || style == 0 || 8 * c0 >= p.rotary_dim) return;
   const float* cs = p.cos_sin + static_cast<int64_t>(pos) * p.rotary_dim;
-  const int half = p.rotary_dim / 2;
-  if (p.rope_style == 1 && c1 >= 0) {
-    rope_neox(x, y, cs, 8 * c0, half);
-  } else if (p.rope_style == 2) {
-    rope_gptj(x, cs, 4 * c0, half);
-  }
+  const bool neox = style == 1;
+  if (neox && c1 < 0) return;
+  rope_unit(x, y, cs, neox ? 8 * c0 : 4 * c0, p.rotary_dim / 2, neox);
 }
 
 // Workgroup (w, y) of the grid: y < Hkv moves K and V of kv head y for the
@@ -313,8 +312,9 @@ __device__ __forceinline__ void rotate_unit(const FillParams& p, int c0, int c1,
 // from registers.  Run tokens' rows go through LDS, and each run is then
 // written in whole lines: K stripe q of its 8 slots (8 x 16 contiguous
 // bytes) and V row d of its 8 slots, the two runs of one page side by side
-// in neighbouring lanes.
-template <int SRC, int DST, int WIN, int MAXC>
+// in neighbouring lanes.  ROPE false: the plain fill (no rotation, no
+// queries), compiled without the rotation code.
+template <int SRC, int DST, int WIN, int MAXC, bool ROPE>
 __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParams p) {
   constexpr int kItems = (WIN * MAXC + kThreads - 1) / kThreads;  // source chunks per thread, at most
   constexpr int EB = elem_bytes<DST>();
@@ -334,9 +334,10 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * WIN;
   const int tid = threadIdx.x;
   const int nwin = static_cast<int>(min(static_cast<int64_t>(WIN), p.num_tokens - t0));
-  const int units = k_units(p);
+  const int style = ROPE ? p.rope_style : 0;
+  const int units = k_units(p, style);
 
-  if (static_cast<int>(blockIdx.y) >= p.num_kv_heads) {
+  if (ROPE && static_cast<int>(blockIdx.y) >= p.num_kv_heads) {
     // ---- queries: rotate and cast head qh of the window's rows (a row is
     // contiguous in and out, so units run fastest: whole lines per wave)
     const int qh = blockIdx.y - p.num_kv_heads;
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
       // which every head re-reads: 1.33x the read bytes)
       const int rot = p.rotary_dim;
       const bool hd_ok = hd == 32 || hd == 64 || hd == 128 || hd == 256;
-      const bool rot_ok = p.rope_style != 1 || (rot >= 8 && rot <= hd && (rot & (rot - 1)) == 0);
+      const bool rot_ok = style != 1 || (rot >= 8 && rot <= hd && (rot & (rot - 1)) == 0);
       if (hd_ok && rot_ok) {
         constexpr int kPieces = (WIN * 32 + kThreads - 1) / kThreads;  // per thread per round (hd <= 128)
         const int lpt = hd / 4;  // pieces of a row; divides the wavefront
@@ -376,15 +377,15 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
             const int it = base + tid + k * kThreads;
             float v[4] = {xq[k][0], xq[k][1], xq[k][2], xq[k][3]};
             float w[4] = {0.f, 0.f, 0.f, 0.f};
-            if (p.rope_style == 1) {  // every lane takes part (a token's lanes are valid together)
+            if (style == 1) {  // every lane takes part (a token's lanes are valid together)
 #pragma unroll
               for (int e = 0; e < 4; ++e) w[e] = __shfl_xor(v[e], rot / 8, kWave);
             }
             if (it < n_items) {
               const int i = it / lpt;
               const int j = it % lpt;
-              if (p.rope_style != 0 && pos[k] >= 0 && pos[k] < p.cos_sin_rows)
-                rope_piece(v, w, p.cos_sin + static_cast<int64_t>(pos[k]) * rot, j, p.rope_style, rot);
+              if (style != 0 && pos[k] >= 0 && pos[k] < p.cos_sin_rows)
+                rope_piece(v, w, p.cos_sin + static_cast<int64_t>(pos[k]) * rot, j, style, rot);
               const u32x2 packed = p.q_out_dtype == kBF16
                                        ? u32x2{Dt<kBF16>::pack2(v[0], v[1]), Dt<kBF16>::pack2(v[2], v[3])}
                                        : u32x2{Dt<kF16>::pack2(v[0], v[1]), Dt<kF16>::pack2(v[2], v[3])};
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
       const int i = it / units;
       if (i < nwin) {
         int c0, c1;
-        unit_chunks(p, it % units, c0, c1);
+        unit_chunks(p, style, it % units, c0, c1);
         const int64_t row = (t0 + i) * q_row + static_cast<int64_t>(qh) * hd;
         rx[k].load(p.q_in, row + 8 * c0);
         if (c1 >= 0) ry[k].load(p.q_in, row + 8 * c1);
@@ -419,11 +420,11 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
       const int i = it / units;
       if (i >= nwin) continue;
       int c0, c1;
-      unit_chunks(p, it % units, c0, c1);
+      unit_chunks(p, style, it % units, c0, c1);
       float x[8], y[8];
       rx[k].to_f32(x);
       if (c1 >= 0) ry[k].to_f32(y);
-      rotate_unit(p, c0, c1, pos[k], pos[k] >= 0 && pos[k] < p.cos_sin_rows, x, y);
+      rotate_unit(p, style, c0, c1, pos[k], pos[k] >= 0 && pos[k] < p.cos_sin_rows, x, y);
       uint16_t* qo = static_cast<uint16_t*>(p.q_out) + (t0 + i) * q_row + static_cast<int64_t>(qh) * hd;
       if (p.q_out_dtype == kBF16) {
         *reinterpret_cast<u32x4*>(qo + 8 * c0) = Store8<kBF16>::pack(x, 1.f);
@@ -450,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
   // halves 32 bytes apart per instruction: 1.26 x the read bytes), and a
   // NeoX rotation over the whole head pairs the lane's own two pieces
   constexpr bool kPieceSrc = SRC == kF32 && DST != kFP8;
-  const bool piece_path = kPieceSrc && (p.rope_style != 1 || p.rotary_dim == hd);
+  const bool piece_path = kPieceSrc && (style != 1 || p.rotary_dim == hd);
   f32x4 pk[kPieceSrc ? kItems : 1][2], pv[kPieceSrc ? kItems : 1][2];
   if constexpr (kPieceSrc) {
     if (piece_path) {
@@ -481,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
     const int i = it / units;
     if (i < nwin) {
       int c0, c1;
-      unit_chunks(p, it % units, c0, c1);
+      unit_chunks(p, style, it % units, c0, c1);
       const int64_t row = (t0 + i) * k_row + static_cast<int64_t>(h) * hd;
       kx[k].load(p.new_k, row + 8 * c0);
       if (c1 >= 0) ky[k].load(p.new_k, row + 8 * c1);
@@ -500,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
       const uint32_t seq = p.q2seq[t];
       pos = p.write_pos[t];
       if (seq < p.num_seqs && pos >= 0 && pos / tpp < p.page_table_width &&
-          (p.rope_style == 0 || pos < p.cos_sin_rows)) {
+          (style == 0 || pos < p.cos_sin_rows)) {
         const uint32_t page = p.page_table[static_cast<int64_t>(seq) * p.page_table_width + pos / tpp];
         if (page < p.num_pages) {
           dpage = page;
@@ -562,8 +563,8 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
         for (int sd = 0; sd < 2; ++sd)
 #pragma unroll
           for (int e = 0; e < 4; ++e) x[sd][e] = pk[k][sd][e];
-        if (p.rope_style != 0)
-          rope_piece_pair(x[0], x[1], p.cos_sin + static_cast<int64_t>(pos_lds[i]) * p.rotary_dim, j, p.rope_style,
+        if (style != 0)
+          rope_piece_pair(x[0], x[1], p.cos_sin + static_cast<int64_t>(pos_lds[i]) * p.rotary_dim, j, style,
                           p.rotary_dim, hd);
         const bool single = kind_lds[i] == 1;
         const int64_t hb = (static_cast<int64_t>(page_lds[i]) * p.num_kv_heads + h) * head_block;
@@ -595,11 +596,11 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
       const int i = it / units;
       if (i < nwin && slot_lds[i] >= 0) {
         int c0, c1;
-        unit_chunks(p, it % units, c0, c1);
+        unit_chunks(p, style, it % units, c0, c1);
         typename Store8<DST>::T a, b;
         bool copied = false;
         if constexpr (SRC == DST) {
-          if (p.rope_style == 0) {  // the reference's fill: a bit copy (NaN payloads included)
+          if (style == 0) {  // the reference's fill: a bit copy (NaN payloads included)
             a = kx[k].w;
             copied = true;
           }
@@ -608,7 +609,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
           float x[8], y[8];
           kx[k].to_f32(x);
           if (c1 >= 0) ky[k].to_f32(y);
-          rotate_unit(p, c0, c1, pos_lds[i], true, x, y);
+          rotate_unit(p, style, c0, c1, pos_lds[i], true, x, y);
           a = Store8<DST>::pack(x, ks_lds[i]);
           if (c1 >= 0) b = Store8<DST>::pack(y, ks_lds[i]);
         }
@@ -717,7 +718,7 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
   }
 }
 
-template <int SRC, int DST, int MAXC>
+template <int SRC, int DST, int MAXC, bool ROPE>
 hipError_t launch_win(const FillParams& p, hipStream_t stream) {
   // small batches (decode fills): windows of 16 tokens, so a 64-token fill
   // still spreads over 4 x 2 Hkv workgroups; prefill batches: 32
@@ -726,10 +727,10 @@ hipError_t launch_win(const FillParams& p, hipStream_t stream) {
   const unsigned gy = p.num_kv_heads + (p.q_in ? p.num_q_heads : 0);
   const size_t lds = 2 * static_cast<size_t>(win) * (p.head_dim * elem_bytes<DST>() + kRowPad);  // K and V rows
   if (win == kLargeWin)
-    hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kLargeWin, MAXC>), dim3(static_cast<unsigned>(windows), gy),
+    hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kLargeWin, MAXC, ROPE>), dim3(static_cast<unsigned>(windows), gy),
                        dim3(kThreads), lds, stream, p);
   else
-    hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kSmallWin, MAXC>), dim3(static_cast<unsigned>(windows), gy),
+    hipLaunchKernelGGL((fill_kv_pages_kernel<SRC, DST, kSmallWin, MAXC, ROPE>), dim3(static_cast<unsigned>(windows), gy),
                        dim3(kThreads), lds, stream, p);
   return hipGetLastError();
 }
@@ -737,8 +738,11 @@ hipError_t launch_win(const FillParams& p, hipStream_t stream) {
 template <int SRC, int DST>
 hipError_t launch_t(const FillParams& p, hipStream_t stream) {
   // per-thread item registers sized for the head dim: up to 128 or up to 256
-  if (p.head_dim <= 128) return launch_win<SRC, DST, 16>(p, stream);
-  return launch_win<SRC, DST, kMaxFillHeadDim / 8>(p, stream);
+  const bool rope = p.rope_style != 0 || p.q_in != nullptr;
+  if (p.head_dim <= 128)
+    return rope ? launch_win<SRC, DST, 16, true>(p, stream) : launch_win<SRC, DST, 16, false>(p, stream);
+  return rope ? launch_win<SRC, DST, kMaxFillHeadDim / 8, true>(p, stream)
+              : launch_win<SRC, DST, kMaxFillHeadDim / 8, false>(p, stream);
 }
 
 template <int SRC>
