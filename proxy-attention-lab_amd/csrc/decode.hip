@@ -360,7 +360,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
   // waits stay exact); when the computed block enters window wcur+1 the
   // windows move up by one, taking the window wcur+2 loaded a step group
   // earlier.
-  int64_t wcur = 0;
+  int wcur = 0;
   uint32_t pid_cur = load_window(c_seq, c_blk, 0), pid_nxt = load_window(c_seq, c_blk, 1),
            pid_later = load_window(c_seq, c_blk, 2);
 
@@ -388,18 +388,20 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     const int hg = min(16, p.group - h0);
     const int qh_base = kvh * p.group + h0;
     const bool complete = (c_blk == 0) && (c_count == c_nb);
-    const int64_t len = c_len;
-    const int64_t n_blk = c_count;
-    const int64_t n_pad = (n_blk + NBUF - 1) / NBUF * NBUF;  // steps of the piece
-    const int64_t bstart = c_blk;                          // first block of the piece
-    const int64_t pbase = (bstart * 16) / TPP;               // its page index
+    // positions inside a piece fit 32 bits (a sequence holds fewer than 2^31
+    // keys), so the per-block bookkeeping is 32-bit arithmetic
+    const int len = static_cast<int>(c_len);
+    const int n_blk = static_cast<int>(c_count);
+    const int n_pad = (n_blk + NBUF - 1) / NBUF * NBUF;  // steps of the piece
+    const int bstart = static_cast<int>(c_blk);        // first block of the piece
+    const int pbase = (bstart * 16) / TPP;             // its page index
     const uint8_t* kbase = static_cast<const uint8_t*>(p.k_pool) + kvh * head_block;
     const uint8_t* vbase = static_cast<const uint8_t*>(p.v_pool) + kvh * head_block;
     const uint8_t* kbase_n = kbase;  // set once the next piece is known
     const uint8_t* vbase_n = vbase;
     int kvh_n = kvh;
-    int64_t nblk_n = 1;
-    int64_t bstart_n = 0, pbase_n = 0;  // first block of the next piece and its page index
+    int nblk_n = 1;
+    int bstart_n = 0, pbase_n = 0;  // first block of the next piece and its page index
 
     // Issue the K and V loads of step i of the piece into buffer `buf`:
     // block i of the piece (clamped to its last block), or, past the
@@ -410,11 +412,11 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     // block is read exactly once per call, so the loads carry the
     // non-temporal hint: the stream does not displace other lines (page ids,
     // partials, the fused op's prefill tiles) from L2 and MALL.
-    auto issue = [&](int64_t i, int buf, uint32_t w_n0) {
+    auto issue = [&](int i, int buf, uint32_t w_n0) {
       const bool to_next = has_next && i >= n_pad;
-      const int64_t j = to_next ? (i - n_pad < nblk_n - 1 ? i - n_pad : nblk_n - 1) : (i < n_blk - 1 ? i : n_blk - 1);
-      const int64_t b = (to_next ? bstart_n : bstart) + j;
-      const int64_t e = (b * 16) / TPP - (to_next ? pbase_n : pbase);  // page within the piece's windows
+      const int j = to_next ? (i - n_pad < nblk_n - 1 ? i - n_pad : nblk_n - 1) : (i < n_blk - 1 ? i : n_blk - 1);
+      const int b = (to_next ? bstart_n : bstart) + j;
+      const int e = (b * 16) / TPP - (to_next ? pbase_n : pbase);  // page within the piece's windows
       // (selects of values, not of variables: a select of two variables'
       // addresses would push the whole pipeline state to scratch)
       const uint32_t w_c = pid_cur, w_x = pid_nxt;
@@ -470,8 +472,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int64_t i, int buf) {
-      const int64_t b = bstart + i;
+    auto compute = [&](int i, int buf) {
+      const int b = bstart + i;
       const bool live = bv[buf] && i < n_blk;  // steps past the piece end are fully masked
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       if constexpr (KV8) {
@@ -506,7 +508,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       // tokens past the end (and whole invalid blocks) are masked: token
       // 4g + e of the block is a key when e < kl (the block's key count is
       // uniform, so the 64-bit part is scalar)
-      const int64_t left = live ? len - b * 16 : 0;
+      const int left = live ? len - b * 16 : 0;
       const int kl = static_cast<int>(left < 16 ? left : 16) - 4 * g;
       float sc4[4];
       float bm = -INFINITY;
@@ -600,9 +602,9 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
       kbase_n = static_cast<const uint8_t*>(p.k_pool) + kvh_x * head_block;
       vbase_n = static_cast<const uint8_t*>(p.v_pool) + kvh_x * head_block;
       kvh_n = kvh_x;
-      nblk_n = x_count;
-      bstart_n = x_blk;
-      pbase_n = (x_blk * 16) / TPP;
+      nblk_n = static_cast<int>(x_count);
+      bstart_n = static_cast<int>(x_blk);
+      pbase_n = (bstart_n * 16) / TPP;
     }
 
     // Every step issues and computes unconditionally (steps past the end
@@ -618,17 +620,17 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     // of each group refreshes (in the first group no issue reaches the next
     // piece: its issues stop at block NBUF + PF - 1 < n_pad).  A piece of one
     // group selects pidn0 and waits once.
-    auto step_group = [&](int64_t i0, uint32_t w_n0) {
+    auto step_group = [&](int i0, uint32_t w_n0) {
       const uint32_t pid_ahead = load_window(c_seq, c_blk, wcur + 2);
 #pragma unroll
       for (int u = 0; u < NBUF; ++u) {
-        const int64_t i = i0 + u;
+        const int i = i0 + u;
         issue(i + PF, (u + PF) % NBUF, w_n0);
         compute(i, u);
       }
       // entered window wcur+1: move the windows up (at most NBUF + PF pages
       // past its start, so no issue has needed window wcur+2 yet)
-      const int64_t e_last = ((bstart + i0 + NBUF - 1) * 16) / TPP - pbase;
+      const int e_last = ((bstart + i0 + NBUF - 1) * 16) / TPP - pbase;
       const bool up = (e_last >> 6) > wcur;
       pid_cur = up ? pid_nxt : pid_cur;
       pid_nxt = up ? pid_later : pid_nxt;
@@ -648,7 +650,7 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
     if (n_pad == NBUF) {
       step_group(0, pidn0);
     } else {
-      int64_t i0 = 0;
+      int i0 = 0;
       do {
         step_group(i0, pidn0_ready);
         i0 += NBUF;
