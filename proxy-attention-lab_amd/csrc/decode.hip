@@ -62,7 +62,8 @@ namespace pal {
 namespace {
 
 constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
-constexpr int kPrefetch = 2;         // blocks whose loads are in flight ahead of the one being computed
+constexpr int kPrefetch = 2;
+constexpr float kLazyMax = 8.f;      // log2 headroom before a decode worker's running max moves         // blocks whose loads are in flight ahead of the one being computed
 constexpr int kGroupThreads = kWorkersPerGroup * kWave;
 constexpr int kPlanThreads = 1024;
 constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each workgroup
@@ -517,17 +518,20 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
         sc4[e] = e < kl ? acc[e] : -INFINITY;
         bm = fmaxf(bm, sc4[e]);
       }
-      bm = max_xor32(max_xor16(bm));  // over the 4 lane groups (scores are finite or -inf)
-      const float m_new = fmaxf(m_run, bm);
-      const float mref = (m_new == -INFINITY) ? 0.f : m_new;  // a head with no key yet: every exponent is -inf
-      if (__ballot(m_new > m_run && m_run != -INFINITY)) {
-        // the max of some head grew: rescale the running state
-        const float alpha = (m_run == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - mref);
+      // The running max of a head moves only when one of its scores passes it
+      // by more than kLazyMax (log2 units), so a block's exponents stay below
+      // 2^kLazyMax and the max over the 4 lane groups and the rescale run
+      // only then; otherwise the block pays one wavefront-uniform test.
+      if (__ballot(bm > m_run + kLazyMax)) {  // (always for a head's first key: m_run = -inf)
+        const float m_new = fmaxf(m_run, max_xor32(max_xor16(bm)));  // scores are finite or -inf
+        // a head with no key yet has l = 0 and O = 0 (alpha 0 keeps them so)
+        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
 #pragma unroll
         for (int n = 0; n < NT; ++n) o[n] *= alpha;
+        m_run = m_new;
       }
-      m_run = m_new;
+      const float mref = (m_run == -INFINITY) ? 0.f : m_run;  // a head with no key yet: every exponent is -inf
       float pe[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
