@@ -237,9 +237,12 @@ def _decode_fp8(case, q, kc, vc, ks, vs, partition=0):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("hd,tpp", [(128, 16), (64, 32), (256, 16)])
+@pytest.mark.parametrize("hd,tpp", [(128, 16), (64, 32), (256, 16), (128, 32), (256, 32)])
 @pytest.mark.parametrize("partition", [0, 512])
 def test_decode_fp8_pages(dtype, hd, tpp, partition):
+    """fp8 pages against the oracle on dequantized pools.  The V codes are read
+    as 16-byte rows (one per 64 dims) at the block's slot offset in its page
+    (0, or 16 on 32-token pages) and transposed across the lane groups."""
     lens = [1, 15, 16, 17, 100, 0, 511, 512, 513, 1000, 2049, 37, 5000]
     rng = np.random.default_rng(hd + tpp + partition)
     case = make_paged_case(hd * 3 + tpp, lens, 16, 4, hd, tpp, dtype)
