@@ -718,8 +718,53 @@ __global__ __launch_bounds__(kThreads) void fill_kv_pages_kernel(const FillParam
   }
 }
 
+// Small batches (a decode step's new tokens): one thread per (token, kv
+// head, 8-dim chunk) copies the chunk's K piece and its 8 V values straight
+// into the pools -- no windows, runs through LDS or barriers; at these sizes
+// coalescing V rows buys nothing and the kernel is its chain of dependent
+// loads.  16-bit pools written from rows of the same dtype (a bit copy).
+constexpr int kTokensThreads = 256;
+constexpr int64_t kSmallFillTokens = 256;  // batches up to this many tokens take it
+__global__ __launch_bounds__(kTokensThreads) void fill_tokens_kernel(const FillParams p) {
+  const int chunks = p.head_dim / 8;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kTokensThreads + threadIdx.x;
+  if (i >= p.num_tokens * p.num_kv_heads * chunks) return;
+  const int c = static_cast<int>(i % chunks);
+  const int64_t th = i / chunks;
+  const int h = static_cast<int>(th % p.num_kv_heads);
+  const int64_t t = th / p.num_kv_heads;
+  const int64_t row = (t * p.num_kv_heads + h) * p.head_dim + 8 * c;
+  const u32x4 kw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.new_k) + row));
+  const u32x4 vw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.new_v) + row));
+  const uint32_t seq = p.q2seq[t];
+  const int pos = p.write_pos[t];
+  const int tpp = p.tokens_per_page;
+  bool ok = seq < p.num_seqs && pos >= 0 && pos / tpp < p.page_table_width;
+  uint32_t page = 0;
+  if (ok) {
+    page = p.page_table[static_cast<int64_t>(seq) * p.page_table_width + pos / tpp];
+    ok = page < p.num_pages;
+  }
+  PAL_DEBUG_FLAG(!ok, kDebugFillDest);
+  if (!ok) return;
+  const int slot = pos % tpp;
+  const int64_t blk = static_cast<int64_t>(page) * p.num_kv_heads + h;  // the (page, kv head) block
+  *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.k_pool) + ((blk * chunks + c) * tpp + slot) * 8) = kw;
+  uint16_t* vp = static_cast<uint16_t*>(p.v_pool) + (blk * p.head_dim + 8 * c) * tpp + slot;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vp[e * tpp] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+}
+
 template <int SRC, int DST, int MAXC, bool ROPE>
 hipError_t launch_win(const FillParams& p, hipStream_t stream) {
+  if constexpr (!ROPE && SRC == DST && DST != kFP8) {
+    if (p.num_tokens <= kSmallFillTokens) {
+      const int64_t n = p.num_tokens * p.num_kv_heads * (p.head_dim / 8);
+      hipLaunchKernelGGL(fill_tokens_kernel, dim3(static_cast<unsigned>((n + kTokensThreads - 1) / kTokensThreads)),
+                         dim3(kTokensThreads), 0, stream, p);
+      return hipGetLastError();
+    }
+  }
   // small batches (decode fills): windows of 16 tokens, so a 64-token fill
   // still spreads over 4 x 2 Hkv workgroups; prefill batches: 32
   const int win = p.num_tokens >= 2048 ? kLargeWin : kSmallWin;
