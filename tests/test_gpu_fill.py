@@ -91,6 +91,22 @@ def test_fill_prefill_chunks_bit_exact(dtype):
     assert np.array_equal(host_bits(v_out), ev)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [256, 257])
+def test_fill_small_batch_threshold_bit_exact(n, dtype):
+    """Batches of up to 256 same-dtype tokens are written one 8-dim chunk per
+    thread, larger ones through the windowed kernel: a run of n consecutive
+    positions from a random start (partial pages at both ends) on both
+    sides of the switch."""
+    announce(f"fill small-batch threshold n={n} {dtype}")
+    kw = _random_fill_case(n, n, 8, 128, 16, 240, 1, 40, consecutive=True)
+    assert len(kw["q2seq"]) == n
+    _, _, k_out, v_out = _run(kw, dtype)
+    ek, ev = orc.fill_kv_pages(**kw)
+    assert np.array_equal(host_bits(k_out), ek)
+    assert np.array_equal(host_bits(v_out), ev)
+
+
 def test_fill_in_place_and_copy_semantics():
     announce("fill in-place vs copy")
     kw = _random_fill_case(9, 20, 2, 64, 16, 12, 2, 4)
