@@ -60,7 +60,16 @@ def _stream_handle(stream, device: torch.device) -> int:
     raise TypeError(f"stream must be None, a torch.cuda.Stream or an int handle, got {type(stream)!r}")
 
 
-def _on_stream(stream_handle: int, device: torch.device):
+def _launch_stream(stream, device: torch.device) -> tuple[int, bool]:
+    """The launch stream's handle, and whether it is torch's current stream
+    (always so for the default ``stream=None``, which then needs no second
+    query in ``_on_stream``)."""
+    if stream is None:
+        return torch.cuda.current_stream(device).cuda_stream, True
+    return _stream_handle(stream, device), False
+
+
+def _on_stream(stream_handle: int, device: torch.device, current: bool = False):
     """Context in which torch work (index conversions, contiguous copies,
     output and workspace allocation) is ordered on the launch stream.
 
@@ -70,7 +79,7 @@ def _on_stream(stream_handle: int, device: torch.device):
     block freed and reused by another stream.  When the launch stream is
     torch's current stream this is a no-op.
     """
-    if stream_handle == torch.cuda.current_stream(device).cuda_stream:
+    if current or stream_handle == torch.cuda.current_stream(device).cuda_stream:
         return contextlib.nullcontext()
     return torch.cuda.stream(torch.cuda.ExternalStream(stream_handle, device=device))
 
@@ -254,8 +263,8 @@ def paged_attention_decode(
         raise ValueError(
             f"[paged_attention_decode] {sequence_lengths.numel()} sequence lengths for {num_seqs} sequences")
     L = _lib.lib()
-    sh = _stream_handle(stream, device)
-    with _on_stream(sh, device):
+    sh, sh_current = _launch_stream(stream, device)
+    with _on_stream(sh, device, sh_current):
         pt = _index_tensor("page_table", page_table, device)
         lens = _index_tensor("sequence_lengths", sequence_lengths, device)
         q = queries.contiguous()
@@ -372,15 +381,15 @@ def fill_kv_pages(
     device, n, num_pages, hkv, hd, tpp, width, num_seqs, pool_code, src_code = _fill_common(
         op, new_keys, new_values, global_key_pool, global_value_pool, page_table, current_token_write_positions,
         query_to_seq_map, k_scales, v_scales)
-    sh = _stream_handle(stream, device)
+    sh, sh_current = _launch_stream(stream, device)
     if copy:
-        with _on_stream(sh, device):
+        with _on_stream(sh, device, sh_current):
             global_key_pool = global_key_pool.clone()
             global_value_pool = global_value_pool.clone()
     if n == 0 or new_keys.numel() == 0:
         return global_key_pool, global_value_pool
     L = _lib.lib()
-    with _on_stream(sh, device):
+    with _on_stream(sh, device, sh_current):
         pt = _index_tensor("page_table", page_table, device)
         pos = _index_tensor("current_token_write_positions", current_token_write_positions, device)
         q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)
@@ -484,8 +493,8 @@ def rope_fill_kv_pages(
         q_code = dtype_code(query_dtype)
     else:
         q_code = _lib.DTYPE_BFLOAT16
-    sh = _stream_handle(stream, device)
-    with _on_stream(sh, device):
+    sh, sh_current = _launch_stream(stream, device)
+    with _on_stream(sh, device, sh_current):
         if queries is not None:
             q_out = torch.empty((n, hq, hd), dtype=query_dtype, device=device)
         if n == 0:
@@ -556,8 +565,8 @@ def paged_attention_prefill(
     if context_len_arr.numel() < num_seqs:
         raise ValueError(f"[{op}] {context_len_arr.numel()} context lengths for {num_seqs} sequences")
     covered = num_seqs * (num_rows // num_seqs) if num_seqs > 0 else 0
-    sh = _stream_handle(stream, device)
-    with _on_stream(sh, device):
+    sh, sh_current = _launch_stream(stream, device)
+    with _on_stream(sh, device, sh_current):
         pt = _index_tensor("page_table", page_table, device)
         ctx = _index_tensor("context_len_arr", context_len_arr, device)
         q = q_prompt.contiguous()
@@ -627,8 +636,8 @@ def paged_attention(
     if query_to_seq_map.numel() != num_rows or query_token_offset.numel() != num_rows:
         raise ValueError(f"[{op}] query_to_seq_map and query_token_offset need one entry per query row ({num_rows})")
     L = _lib.lib()
-    sh = _stream_handle(stream, device)
-    with _on_stream(sh, device):
+    sh, sh_current = _launch_stream(stream, device)
+    with _on_stream(sh, device, sh_current):
         pt = _index_tensor("page_table", page_table, device)
         lens = _index_tensor("sequence_lengths", sequence_lengths, device)
         q2s = _index_tensor("query_to_seq_map", query_to_seq_map, device)

@@ -120,7 +120,7 @@ class PagePool:
         the GPU, then rewrite every page table in ``page_tables`` (uint32 /
         int32 device tensors, updated in place) through the same map.  Every
         argument is checked before the first launch."""
-        from .ops import _on_stream, _stream_handle
+        from .ops import _launch_stream, _on_stream
 
         page_tables = tuple(page_tables)
         PagePool._check_targets(k_pool, v_pool, page_tables, k_scales, v_scales)
@@ -137,8 +137,8 @@ class PagePool:
         remap = np.arange(num_pages, dtype=np.uint32)
         remap[src[src < num_pages]] = dst[src < num_pages]
         L = _lib.lib()
-        sh = _stream_handle(stream, device)
-        with _on_stream(sh, device):
+        sh, sh_current = _launch_stream(stream, device)
+        with _on_stream(sh, device, sh_current):
             s_d = torch.from_numpy(src.view(np.int32)).to(device, non_blocking=False)
             d_d = torch.from_numpy(dst.view(np.int32)).to(device, non_blocking=False)
             r_d = torch.from_numpy(remap.view(np.int32)).to(device, non_blocking=False)
