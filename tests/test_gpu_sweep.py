@@ -55,6 +55,19 @@ def _fit(lens, hq, hd):
     return lens
 
 
+def _pools(case, rng, fp8):
+    """The case's pools on the device and as the oracle takes them: its 16-bit
+    pools, or fp8 codes with per-(page, kv head) scales.  Returns (k_pool,
+    v_pool, scale kwargs of the op, (k, v) for the oracle, kv_scales for the
+    oracle)."""
+    if not fp8:
+        return (dev_bits(case.k_pool, case.dtype), dev_bits(case.v_pool, case.dtype), {},
+                (case.k_pool, case.v_pool), None)
+    kc, vc, ks, vs = fp8_case(case, rng)
+    scales = dict(k_scales=torch.from_numpy(ks).to(DEV), v_scales=torch.from_numpy(vs).to(DEV))
+    return dev_codes(kc), dev_codes(vc), scales, (kc, vc), (ks, vs)
+
+
 def _decode_case(i):
     rng = np.random.default_rng(1000 + i)
     dtype = "bf16" if rng.random() < 0.6 else "f16"
@@ -104,14 +117,15 @@ def test_prefill_sweep(i):
     hist = _fit(_lens(rng, int(rng.integers(1, 6)), 3000), hq, hd)
     while len(hist) * plen * (max(hist) + plen) * hq * hd > 4 * BUDGET and plen > 1:
         plen //= 2
+    fp8 = rng.random() < 0.5 and hd in (64, 128, 256) and tpp in (16, 32)
     case, q, k, v = make_prefill_case(4000 + i, hist, plen, hq, hkv, hd, tpp, dtype)
-    what = f"prefill sweep {i}: {dtype} Hq={hq} Hkv={hkv} HD={hd} TPP={tpp} P={plen} hist={hist}"
+    what = f"prefill sweep {i}: {dtype} fp8={fp8} Hq={hq} Hkv={hkv} HD={hd} TPP={tpp} P={plen} hist={hist}"
     announce(what)
-    out = pal.paged_attention_prefill(dev_bits(q, dtype), dev_bits(k, dtype), dev_bits(v, dtype),
-                                      dev_bits(case.k_pool, dtype), dev_bits(case.v_pool, dtype),
-                                      dev_index(case.page_table, torch.uint32), dev_index(case.seq_lens))
+    kp, vp, scales, (ko, vo), kvs = _pools(case, rng, fp8)
+    out = pal.paged_attention_prefill(dev_bits(q, dtype), dev_bits(k, dtype), dev_bits(v, dtype), kp, vp,
+                                      dev_index(case.page_table, torch.uint32), dev_index(case.seq_lens), **scales)
     torch.cuda.synchronize()
-    ref = orc.paged_attention_prefill(q, k, v, case.k_pool, case.v_pool, case.page_table, case.seq_lens, dtype)
+    ref = orc.paged_attention_prefill(q, k, v, ko, vo, case.page_table, case.seq_lens, dtype, kv_scales=kvs)
     assert_close(host_f32(out), ref, dtype, what)
 
 
@@ -129,15 +143,17 @@ def test_fused_sweep(i):
         dec = [int(rng.integers(1, 2000))]
     dec = _fit(dec, hq, hd) if dec else dec
     block = int(rng.choice([16, 32, 64, 128]))
+    fp8 = rng.random() < 0.5 and hd in (64, 128, 256)
     fc = make_fused_case(6000 + i, dec, chunks, hq, hkv, hd, tpp, dtype, block=block)
     c = fc.case
-    what = (f"fused sweep {i}: {dtype} Hq={hq} Hkv={hkv} HD={hd} TPP={tpp} block={block} decode={dec} "
+    what = (f"fused sweep {i}: {dtype} fp8={fp8} Hq={hq} Hkv={hkv} HD={hd} TPP={tpp} block={block} decode={dec} "
             f"chunks={chunks}")
     announce(what)
-    out = pal.paged_attention(dev_bits(fc.queries, dtype), dev_bits(c.k_pool, dtype), dev_bits(c.v_pool, dtype),
-                              dev_index(c.page_table, torch.uint32), dev_index(c.seq_lens),
-                              dev_index(fc.q2seq, torch.uint32), dev_index(fc.q_offset))
+    kp, vp, scales, (ko, vo), kvs = _pools(c, rng, fp8)
+    out = pal.paged_attention(dev_bits(fc.queries, dtype), kp, vp, dev_index(c.page_table, torch.uint32),
+                              dev_index(c.seq_lens), dev_index(fc.q2seq, torch.uint32), dev_index(fc.q_offset),
+                              **scales)
     torch.cuda.synchronize()
-    ref = orc.paged_attention(fc.queries, c.k_pool, c.v_pool, c.page_table, c.seq_lens, fc.q2seq, fc.q_offset,
-                              dtype)
+    ref = orc.paged_attention(fc.queries, ko, vo, c.page_table, c.seq_lens, fc.q2seq, fc.q_offset, dtype,
+                              kv_scales=kvs)
     assert_close(host_f32(out), ref, dtype, what)
