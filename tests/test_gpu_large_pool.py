@@ -179,3 +179,36 @@ def test_large_pool_copy_pages():
     assert np.array_equal(host_bits(k[base:]), ek)
     assert np.array_equal(host_bits(v[base:]), ev)
     assert np.array_equal(pt.view(torch.int32).cpu().numpy().view(np.uint32).astype(np.int64) - base, remap[table])
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_large_pool_rope_fill(kv):
+    """The RoPE fill (fp32 rows, NeoX, queries rotated too) into pages past the
+    5 GiB mark: pools and rotated queries bit-exact."""
+    from test_gpu_fp8_rope import dev_f32, dev_pool, fill_layout, host_pool, src_values
+
+    hkv, hq, hd, tpp = 4, 16, 128, 16
+    k, v, pt, pos, q2s, (ks, vs) = fill_layout(97, hkv, hd, tpp, kv)
+    rng = np.random.default_rng(97)
+    n = len(pos)
+    nk = src_values(rng, (n, hkv, hd), "f32", 2.0)
+    nv = src_values(rng, (n, hkv, hd), "f32", 2.0)
+    q = src_values(rng, (n, hq, hd), "f32", 2.0)
+    table = pal.rope_cos_sin_cache(512, hd, 10000.0, device=DEV)
+    base = _base(k)
+    announce(f"large pool rope fill {kv} base page {base}")
+    kd, vd = _big(dev_pool(k, kv), base), _big(dev_pool(v, kv), base)
+    extra = {}
+    if kv == "fp8":
+        extra = dict(k_scales=_big(torch.from_numpy(ks).to(DEV), base),
+                     v_scales=_big(torch.from_numpy(vs).to(DEV), base))
+    _, _, qo = pal.rope_fill_kv_pages(dev_f32(nk, "f32"), dev_f32(nv, "f32"), kd, vd, _shifted(pt, base),
+                                      dev_index(pos), dev_index(q2s, torch.uint32), table, queries=dev_f32(q, "f32"),
+                                      rotary_dim=hd, style="neox", query_dtype=torch.bfloat16, **extra)
+    torch.cuda.synchronize()
+    ek, ev, eq = orc.fill_kv_pages_ex(nk, nv, k, v, kv, pt, pos, q2s, k_scales=ks if kv == "fp8" else None,
+                                      v_scales=vs if kv == "fp8" else None, rope=(table.cpu().numpy(), hd, "neox"),
+                                      queries=q, q_out_dtype="bf16")
+    assert np.array_equal(host_pool(kd[base:], kv), ek), "K pool differs"
+    assert np.array_equal(host_pool(vd[base:], kv), ev), "V pool differs"
+    assert np.array_equal(host_bits(qo), eq), "rotated queries differ"
