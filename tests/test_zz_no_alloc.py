@@ -60,6 +60,46 @@ def test_noalloc_matches_workspace_entry_two_calls(partition):
         assert_close(host_f32(got), ref, "bf16", f"noalloc {what} partition {partition}")
 
 
+def test_noalloc_under_graph_capture():
+    """The callers the entry is for: captured into a HIP graph (after one
+    eager call, which reads the scratch array's address) and replayed with
+    new queries between replays; every replay equals the workspace entry's
+    eager output bit for bit."""
+    case = make_paged_case(92, [3000, 17, 512, 4096, 1, 900], 32, 8, 128, 16, "bf16")
+    rng = np.random.default_rng(92)
+    k, v = dev_bits(case.k_pool, "bf16"), dev_bits(case.v_pool, "bf16")
+    pt, lens = dev_index(case.page_table, torch.uint32), dev_index(case.seq_lens)
+    q = dev_bits(randn_bits(rng, (case.num_seqs, 32, 128), "bf16"), "bf16")
+    out = torch.empty_like(q)
+    L = _lib.lib()
+
+    def call():
+        _lib.check(L.pal_paged_attention_decode_noalloc(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), pt.data_ptr(), lens.data_ptr(), out.data_ptr(),
+            _lib.DTYPE_BFLOAT16, case.num_seqs, case.num_seqs, 32, 8, 128, 16, int(case.k_pool.shape[0]),
+            int(case.page_table.shape[1]), 0, torch.cuda.current_stream().cuda_stream))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    announce("noalloc decode under graph capture")
+    with torch.cuda.graph(g, stream=side):
+        call()
+    torch.cuda.synchronize()
+    for r in range(3):
+        q.copy_(dev_bits(randn_bits(rng, (case.num_seqs, 32, 128), "bf16"), "bf16"))
+        torch.cuda.synchronize()
+        announce(f"noalloc graph replay {r}")
+        g.replay()
+        torch.cuda.synchronize()
+        eager = pal.paged_attention_decode(q, k, v, pt, lens)
+        torch.cuda.synchronize()
+        assert np.array_equal(host_bits(out), host_bits(eager)), f"replay {r} differs from the workspace entry"
+
+
 def test_noalloc_rejects_shapes_beyond_scratch():
     """A partition-128 call over 4096 sequences with 8192-page tables needs
     far more than the 64 MiB array: rejected with a clear error.  The
