@@ -83,6 +83,13 @@ struct StepGeo {
 // contiguous; the V groups are swizzled by row so that the PV operand reads
 // (one 16-byte chunk per lane and row) spread over all banks.
 __device__ __forceinline__ int kperm(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+// fp8 steps: QK operand row m holds key 16 b2 + 8 b4 + 4 b3 + (m & 3) (b_i:
+// bit i of m), so that the scores a lane holds after the QK product are
+// the 16 consecutive keys 16 h .. 16 h + 15 (h: its lane half) in register
+// order, and one 16-byte V item (16 keys of one row) feeds both PV k-steps.
+__device__ __forceinline__ int kperm_f8(int m) {
+  return ((m & 4) << 2) | ((m & 16) >> 1) | ((m & 8) >> 1) | (m & 3);
+}
 
 template <int HD, int TPP>
 struct ItemMap {
@@ -158,9 +165,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   using IM = ItemMap<HD, TP>;
   // fp8 pools in window mode: steps are copied as fp8 bytes (16-byte items:
   // 16 dims of one key for K, 16 keys of one row for V; 2 HD items each, in
-  // item order) and converted in the operand reads.  A copy instruction must
-  // stay in one page: with TP 16 that needs HD % 64 == 0 (every fp8 pool's
-  // head dim).
+  // item order) and converted in the operand reads, each lane reading whole
+  // items: a K item gives the 8 dims of two QK k-steps, a V item the 8 keys
+  // of both PV k-steps (the keys of an fp8 step are in kperm_f8 order, the
+  // query operand permuted to match).  A copy instruction must stay in one
+  // page: with TP 16 that needs HD % 64 == 0 (every fp8 pool's head dim).
   constexpr bool F8 = KV8 && !PROMPT && (TP == 32 || HD % 64 == 0);
   constexpr int NI8 = 2 * HD;
   constexpr int NL8 = (NI8 + kPfThreads - 1) / kPfThreads;
@@ -213,10 +222,19 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   {
     const int64_t qrow = static_cast<int64_t>(row0 + (row_ok ? my_t : 0)) * p.num_q_heads + kvh * p.group + h0 +
                          (row_ok ? my_h : 0);
-    const uint16_t* qp = p.q + qrow * HD + 8 * half;
     const uint32_t qmask = row_ok ? 0xFFFFFFFFu : 0u;
+    if constexpr (F8) {
+      // fp8 steps read 16 dims of stripe 2j + half per K item: k-step 2j + e
+      // of this lane half takes dims 16 (2j + half) + 8e .. +7
+      const uint16_t* qp = p.q + qrow * HD + 16 * half;
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qv[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk) & qmask;
+      for (int kk = 0; kk < KS; ++kk)
+        qv[kk] = *reinterpret_cast<const u32x4*>(qp + 32 * (kk / 2) + 8 * (kk % 2)) & qmask;
+    } else {
+      const uint16_t* qp = p.q + qrow * HD + 8 * half;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) qv[kk] = *reinterpret_cast<const u32x4*>(qp + 16 * kk) & qmask;
+    }
   }
   const uint32_t* pt = p.page_table + s * p.page_table_width;
   constexpr int kPidPre = kPidChunk / kPfThreads;  // entries of chunk 0 per thread
@@ -343,26 +361,20 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // 16c+15), key of the step; V item i: page half ph (TP 16) or 16-key half
   // of the page row (TP 32), row d.  Item i is LDS slot i.
   auto k8_item = [](int i, int& ph, int& c, int& key) {
-    if (TP == 16) {
+    if (TP == 16) {  // page-major; page 1's keys at positions XOR 12, so a 16-lane operand read spans all banks
       ph = i / HD;
       c = (i % HD) / 16;
-      key = 16 * ph + i % 16;
-    } else {
+      key = 16 * ph + ((i % 16) ^ (ph ? 12 : 0));
+    } else {  // operand row order: slot 32 c + m holds key kperm_f8(m)
       ph = 0;
       c = i / 32;
-      key = i % 32;
+      key = kperm_f8(i % 32);
     }
   };
   auto v8_item = [](int i, int& ph, int& d, int& kb) {  // kb: the item's first key in the step
-    if (TP == 16) {
-      ph = i / HD;
-      d = i % HD;
-      kb = 16 * ph;
-    } else {
-      ph = 0;
-      d = i / 2;
-      kb = 16 * (i % 2);
-    }
+    ph = TP == 16 ? i / HD : 0;
+    d = i % HD;
+    kb = 16 * (i / HD);
   };
   const uint8_t* k8_pool = reinterpret_cast<const uint8_t*>(p.k_pool) + kv_head_off8;
   const uint8_t* v8_pool = reinterpret_cast<const uint8_t*>(p.v_pool) + kv_head_off8;
@@ -718,7 +730,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
       float s0, s1;
       read_scales(ks_lds, j, s0, s1);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[r] *= r < 8 ? s0 : s1;
+      for (int r = 0; r < 16; ++r) sacc[r] *= half ? s1 : s0;  // the lane's keys are 16 half .. +15
     }
   };
   auto read_pids = [&](int j) {
@@ -749,13 +761,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // S^T[key][M-row] = sum_d K[key][d] Q[M-row][d] for step st (raw scores).
   auto read_k = [&](int st, u32x4 (&ka)[KS]) {
     const int buf = st % kNBuf;
-    if constexpr (F8) {  // lane: key kperm(col), 8 dims of stripe kk (exact in 16 bits; the scale goes on the scores)
-      const int key = kperm(col);
+    if constexpr (F8) {  // lane: key kperm_f8(col), all 16 dims of stripe 2j + half: k-steps 2j and 2j + 1
+      const int key = kperm_f8(col);
       const uint8_t* kb = reinterpret_cast<const uint8_t*>(k_lds(buf));
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const int slot = TP == 16 ? (key / 16) * HD + kk * 16 + key % 16 : kk * 32 + key;
-        ka[kk] = fp8x8_exact<DT>(*reinterpret_cast<const u32x2*>(kb + slot * 16 + 8 * half));
+      for (int j = 0; j < KS / 2; ++j) {
+        const int c = 2 * j + half;
+        const int slot = TP == 16 ? (key / 16) * HD + c * 16 + ((key % 16) ^ (key >= 16 ? 12 : 0)) : c * 32 + col;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(kb + slot * 16);
+        // exact in 16 bits; the K scale goes on the scores
+        ka[2 * j] = fp8x8_exact<DT>(u32x2{v.x, v.y});
+        ka[2 * j + 1] = fp8x8_exact<DT>(u32x2{v.z, v.w});
       }
       return;
     }
@@ -777,7 +793,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // exp2 past ~2^31.  An exact (s - m) * scale_log2 costs 16 more VALU
   // instructions per step (a rarely taken branch to it: 3 % on config 4).
   auto mask_score = [&](f32x16& sacc, int r, int st) {
-    const int key = st * kKeys + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+    const int key = F8 ? st * kKeys + 16 * half + r : st * kKeys + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
     if (key >= my_lim) sacc[r] = -INFINITY;
   };
   // Given this lane's max bm of a step's scores: moves the running max to the
@@ -896,7 +912,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
     for (int r = 0; r < 16; ++r) s_next[r] = 0.f;
     u32x4 va[KS];  // PV operand m: k-step m / DT32, row tile m % DT32 (KS == 2 * DT32)
-    u32x2 v8[F8 ? KS : 1];  // fp8: the raw bytes of each chunk's V operand
+    u32x4 v16[F8 ? DT32 : 1];  // fp8: row tile t's item (16 keys of one row), both PV k-steps
     uint32_t pp[8];  // packed probabilities of the lane's scores 2q, 2q+1
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
@@ -913,19 +929,24 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
         const u32x2 lo = lds_read_tr16(vr);           // keys kg .. kg+3
         const u32x2 hi = lds_read_tr16(vr + 4 * HD);  // keys kg+4 .. kg+7 (vd_swz(key + 4) = vd_swz(key))
         va[kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      } else if constexpr (F8) {  // row d = col + 32 (kk % DT32), keys 16 g + 8 half .. +7 of item (g, d)
-        const int g = kk / DT32;
-        const int d = col + 32 * (kk % DT32);
-        const int slot = TP == 16 ? g * HD + d : d * 2 + g;
-        // exact in 16 bits; the V scale is on P.  Chunk kk converts the
-        // operand read in chunk kk - 1 (its LDS read has landed by then) and
-        // consumes it there, so the conversions are not sunk to the PV MFMAs.
-        v8[kk] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) + slot * 16 + 8 * half);
-        if (kk > 0) {
-          va[kk - 1] = fp8x8_exact<DT>(v8[kk - 1]);
+      } else if constexpr (F8) {
+        // chunk t < DT32 reads row tile t's item (half, d = col + 32 t): keys
+        // 16 half .. +7 for k-step 0 (operand t), +8 .. +15 for k-step 1
+        // (operand t + DT32).  Exact in 16 bits; the V scale is on P.  Each
+        // half is converted in a later chunk than its read (the LDS read has
+        // landed) and consumed there, so the conversions are not sunk to the
+        // PV MFMAs.
+        if (kk < DT32)
+          v16[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(v_lds(vbuf)) +
+                                                    (half * HD + col + 32 * kk) * 16);
+        if (kk >= 1 && kk <= DT32) {
+          va[kk - 1] = fp8x8_exact<DT>(u32x2{v16[kk - 1].x, v16[kk - 1].y});
           asm volatile("" ::"v"(va[kk - 1]));
         }
-        if (kk == KS - 1) va[kk] = fp8x8_exact<DT>(v8[kk]);
+        if (kk >= DT32) {
+          va[kk] = fp8x8_exact<DT>(u32x2{v16[kk - DT32].z, v16[kk - DT32].w});
+          asm volatile("" ::"v"(va[kk]));
+        }
       } else {
         va[kk] = *reinterpret_cast<const u32x4*>(v_lds(vbuf) + (v_base[kk / DT32] + (kk % DT32) * IM::kVRowTile) * 8);
       }
@@ -934,7 +955,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
 #pragma unroll
       for (int q = kk * 8 / KS; q < (kk + 1) * 8 / KS; ++q) {
         if constexpr (F8) {  // the exp-sum of the probabilities, then P times its key's page V scale
-          const float sv = (TP == 16 && q >= 4) ? vs1 : vs0;
+          const float sv = half ? vs1 : vs0;  // the lane's keys 16 half .. +15: page half (TP 32: vs1 == vs0)
           l_run += pe[2 * q] + pe[2 * q + 1];
           pp[q] = Dt<DT>::pack2(pe[2 * q] * sv, pe[2 * q + 1] * sv);
         } else {
