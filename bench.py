@@ -22,6 +22,9 @@ The other configs are reported beside it, each in its own object:
       rows, interleaved in shuffled row blocks, one operator call
   lh  batch-1 decode over 131,072 / 524,288 / 1,048,576-token histories
       (the reference benchmark's range), 32/16 heads, HD 128, bf16
+  pages  (not in the default run) config 2's decode at head dims 64, 128
+      and 256 over 16- and 32-token pages, 16-bit and fp8 pools, both split
+      forms, each over 4 rotated copies
 The CPU baseline is the reference's equivalency computation (gather pages +
 fp32 softmax attention) on torch CPU over the host cores: configs 1 and 2 in
 full, configs 3-5 on a stated subsample scaled by its share of the work.
@@ -809,6 +812,35 @@ def run_extra(configs: set[str], dev, args, samples: dict | None = None) -> dict
         torch.cuda.empty_cache()
     if "lh" in configs:
         out["long_history_decode"] = run_long_history(dev, min(steps, 10), warm, stream)
+    if "pages" in configs:
+        out["decode_page_sizes"] = run_page_sizes(dev, steps, warm, stream)
+    return out
+
+
+def run_page_sizes(dev, steps: int, warm: int, stream) -> dict:
+    """Config 2's decode (64 seqs, U[512,4096] ctx, 32/8 heads) at head dims
+    64 / 128 / 256 over 16- and 32-token pages: bf16 pools in both split
+    forms and fp8 pools, each timed over 4 rotated copies."""
+    out = {"workload": "config 2's shape (64 seqs, U[512,4096] ctx, 32/8 heads, bf16 queries) at head dims 64, 128, "
+                       "256 over 16- and 32-token pages; 4 rotated copies per point"}
+    for hd in (64, 128, 256):
+        for tpp in (16, 32):
+            ws = [DecodeWorkload(seed=i, hd=hd, tpp=tpp, device=dev) for i in range(4)]
+            nbytes = float(np.mean([w.decode_bytes() for w in ws]))
+            rec = {}
+            for part in (0, 512):
+                ms = time_rotated([lambda w=w, part=part: w.decode(part) for w in ws], steps, warm, stream)
+                rec[f"bf16_partition_{part}"] = {"us": round(ms * 1e3, 1),
+                                                 "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            for w in ws:
+                w.make_fp8()
+            f8 = float(np.mean([w.decode_bytes_fp8() for w in ws]))
+            ms = time_rotated([w.decode_fp8 for w in ws], steps, warm, stream)
+            rec["fp8_partition_0"] = {"us": round(ms * 1e3, 1),
+                                      "frac_of_hbm_peak": round(f8 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            out[f"hd{hd}_tpp{tpp}"] = rec
+            del ws
+            torch.cuda.empty_cache()
     return out
 
 

@@ -62,8 +62,22 @@ namespace pal {
 namespace {
 
 constexpr int kWorkersPerGroup = 4;  // independent wavefront workers per workgroup
-constexpr int kPrefetch = 2;
-constexpr float kLazyMax = 8.f;      // log2 headroom before a decode worker's running max moves         // blocks whose loads are in flight ahead of the one being computed
+constexpr int kPrefetch = 2;         // blocks whose loads are in flight ahead of the one being computed
+constexpr float kLazyMax = 8.f;      // log2 headroom before a decode worker's running max moves
+
+// A K/V load of a 16-token block.  With 32-token pages a block reads half of
+// each V row and of each K stripe row of its page, and the next block (the
+// same wavefront, one step later) the other half; when a (page, kv head)
+// block holds 8 KiB or more (16-bit pools from head dim 128, fp8 pools at
+// head dim 256) the loads are cacheable so that half stays in L2 for it
+// (config 2's shape over 32-token pages: head dim 128 138 -> 118 us, 256 288
+// -> 228 us, fp8 head dim 256 146 -> 126 us); smaller blocks, and 16-token
+// pages, whose blocks read whole rows, stream non-temporally.
+template <int TPP, int kBlockBytes, typename T>
+__device__ __forceinline__ T page_load(const T* p) {
+  if constexpr (TPP == 32 && kBlockBytes >= 8192) return *p;
+  else return __builtin_nontemporal_load(p);
+}
 constexpr int kGroupThreads = kWorkersPerGroup * kWave;
 constexpr int kPlanThreads = 1024;
 constexpr int kInlinePlanSeqs = 1024;  // largest batch scanned into LDS by each workgroup
@@ -439,7 +453,8 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
 #pragma unroll
         for (int j = 0; j < KL8; ++j) {
           const int c = g + 4 * j;  // stripe of dims 16c .. 16c+15
-          kb4[buf][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
+          kb4[buf][j] =
+              page_load<TPP, HD * TPP * EB>(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
         }
         // V: lane 16g + i reads the block's 16 codes of dim row 64q + 16g + i
         // (one 16-byte load per 64 rows instead of four 4-byte ones); compute
@@ -447,23 +462,25 @@ __device__ __forceinline__ void process_range(const DecodeParams& p, const Sched
         const uint8_t* vrow = (to_next ? vb_x : vbase) + static_cast<int64_t>(page) * page_stride + slot0;
 #pragma unroll
         for (int q = 0; q < NT / 4; ++q)
-          vq8[buf][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow + (64 * q + 16 * g + r16) * TPP));
+          vq8[buf][q] =
+              page_load<TPP, HD * TPP * EB>(reinterpret_cast<const u32x4*>(vrow + (64 * q + 16 * g + r16) * TPP));
       } else {
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
           if constexpr (kK32) {
             const int c = 4 * kk + g;  // stripe holding dims 32kk + 8g .. +7
             kb4[buf][kk] =
-                __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
+                page_load<TPP, HD * TPP * EB>(reinterpret_cast<const u32x4*>(kp + (c * TPP + slot0 + r16) * 16));
           } else {
             const int d = 16 * kk + 4 * g;  // dims d .. d+3
-            kb2[buf][kk] = __builtin_nontemporal_load(
+            kb2[buf][kk] = page_load<TPP, HD * TPP * EB>(
                 reinterpret_cast<const u32x2*>(kp + (((d >> 3) * TPP + slot0 + r16) * 8 + (d & 7)) * 2));
           }
         }
 #pragma unroll
         for (int n = 0; n < NT; ++n)
-          vb[buf][n] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP * 2));
+          vb[buf][n] =
+              page_load<TPP, HD * TPP * EB>(reinterpret_cast<const u32x2*>(vp + (16 * n + r16) * TPP * 2));
       }
     };
 
