@@ -25,6 +25,8 @@ The other configs are reported beside it, each in its own object:
   pages  (not in the default run) config 2's decode at head dims 64, 128
       and 256 over 16- and 32-token pages, 16-bit and fp8 pools, both split
       forms, each over 4 rotated copies
+  shapes  (not in the default run) bf16 decode, HD 128, 16-token pages,
+      across batch shapes and GQA groups, both split forms
 The CPU baseline is the reference's equivalency computation (gather pages +
 fp32 softmax attention) on torch CPU over the host cores: configs 1 and 2 in
 full, configs 3-5 on a stated subsample scaled by its share of the work.
@@ -814,6 +816,38 @@ def run_extra(configs: set[str], dev, args, samples: dict | None = None) -> dict
         out["long_history_decode"] = run_long_history(dev, min(steps, 10), warm, stream)
     if "pages" in configs:
         out["decode_page_sizes"] = run_page_sizes(dev, steps, warm, stream)
+    if "shapes" in configs:
+        out["decode_shapes"] = run_decode_shapes(dev, steps, warm, stream)
+    return out
+
+
+DECODE_SHAPES = [  # (name, DecodeWorkload arguments)
+    ("config 2: 64 seqs U[512,4096], 32/8 heads", {}),
+    ("512 seqs U[64,512]", dict(num_seqs=512, ctx_lo=64, ctx_hi=512)),
+    ("2048 seqs U[16,256]", dict(num_seqs=2048, ctx_lo=16, ctx_hi=256)),
+    ("4096 seqs U[256,1024]", dict(num_seqs=4096, ctx_lo=256, ctx_hi=1024)),
+    ("64 seqs, 32/32 heads (no GQA)", dict(hq=32, hkv=32)),
+    ("64 seqs, 64/8 heads", dict(hq=64, hkv=8)),
+    ("64 seqs, 8/8 heads", dict(hq=8, hkv=8)),
+    ("8 seqs x 32768", dict(num_seqs=8, ctx_lo=32768, ctx_hi=32768)),
+]
+
+
+def run_decode_shapes(dev, steps: int, warm: int, stream) -> dict:
+    """bf16 decode (HD 128, 16-token pages) across batch shapes and GQA
+    groups, both split forms, each over 4 rotated copies."""
+    out = {"workload": "bf16 decode, HD 128, 16-token pages, permuted pages; 4 rotated copies per shape"}
+    for name, kw in DECODE_SHAPES:
+        ws = [DecodeWorkload(seed=i, device=dev, **kw) for i in range(4)]
+        nbytes = float(np.mean([w.decode_bytes() for w in ws]))
+        rec = {"bytes": int(nbytes)}
+        for part in (0, 512):
+            ms = time_rotated([lambda w=w, part=part: w.decode(part) for w in ws], steps, warm, stream)
+            rec[f"partition_{part}"] = {"us": round(ms * 1e3, 1),
+                                        "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        out[name] = rec
+        del ws
+        torch.cuda.empty_cache()
     return out
 
 
