@@ -367,6 +367,31 @@ def test_fused_fp8_pages(dtype, hd, tpp):
     assert_close(host_f32(out), ref, dtype, f"fp8 fused {dtype} hd{hd} tpp{tpp}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_fused_fp8_query_magnitudes(dtype):
+    """fp8 pages under the fused op with query heads across the dtype's range
+    (zeros, tiny, large, mixed, near the range ends; the large heads held to
+    the tiles' exact range), in its decode rows and its tiles."""
+    from pal_cases import make_fused_case
+
+    rng = np.random.default_rng(75)
+    fc = make_fused_case(75, [5, 300, 1200], [(0, 70), (200, 130)], 16, 4, 128, 16, dtype)
+    fc.queries = extreme_query_bits(rng, fc.queries.shape, dtype, tiles=True)
+    c = fc.case
+    kc, vc, ks, vs = fp8_case(c, rng)
+    announce(f"fused fp8 pages, query magnitudes {dtype}")
+    out = pal.paged_attention(dev_bits(fc.queries, dtype), dev_codes(kc), dev_codes(vc),
+                              dev_index(c.page_table, torch.uint32), dev_index(c.seq_lens),
+                              dev_index(fc.q2seq, torch.uint32), dev_index(fc.q_offset),
+                              k_scales=torch.from_numpy(ks).to(DEV), v_scales=torch.from_numpy(vs).to(DEV))
+    torch.cuda.synchronize()
+    got = host_f32(out)
+    ref = orc.paged_attention(fc.queries, kc, vc, c.page_table, c.seq_lens, fc.q2seq, fc.q_offset, dtype,
+                              kv_scales=(ks, vs))
+    assert np.isfinite(got).all()
+    assert_close(got, ref, dtype, f"fp8 fused query magnitudes {dtype}")
+
+
 def test_fused_fp8_claiming_mode():
     """More than 2048 lone rows with keys over fp8 pages at head_dim 128: the
     fused kernel's decode workers claim row batches and compute rows whole."""
