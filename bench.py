@@ -24,7 +24,8 @@ The other configs are reported beside it, each in its own object:
       (the reference benchmark's range), 32/16 heads, HD 128, bf16
   pages  (not in the default run) config 2's decode at head dims 64, 128
       and 256 over 16- and 32-token pages, 16-bit and fp8 pools, both split
-      forms, each over 4 rotated copies
+      forms, each over 4 rotated copies; config 4's attention at the same
+      head dims and page sizes over 3 rotated copies
   shapes  (not in the default run) bf16 decode, HD 128, 16-token pages,
       across batch shapes and GQA groups, both split forms
 The CPU baseline is the reference's equivalency computation (gather pages +
@@ -856,7 +857,8 @@ def run_page_sizes(dev, steps: int, warm: int, stream) -> dict:
     64 / 128 / 256 over 16- and 32-token pages: bf16 pools in both split
     forms and fp8 pools, each timed over 4 rotated copies."""
     out = {"workload": "config 2's shape (64 seqs, U[512,4096] ctx, 32/8 heads, bf16 queries) at head dims 64, 128, "
-                       "256 over 16- and 32-token pages; 4 rotated copies per point"}
+                       "256 over 16- and 32-token pages, 4 rotated copies per point; config4_attention: config 4's "
+                       "chunked prefill at the same head dim and page size, 3 rotated copies"}
     for hd in (64, 128, 256):
         for tpp in (16, 32):
             ws = [DecodeWorkload(seed=i, hd=hd, tpp=tpp, device=dev) for i in range(4)]
@@ -872,8 +874,13 @@ def run_page_sizes(dev, steps: int, warm: int, stream) -> dict:
             ms = time_rotated([w.decode_fp8 for w in ws], steps, warm, stream)
             rec["fp8_partition_0"] = {"us": round(ms * 1e3, 1),
                                       "frac_of_hbm_peak": round(f8 / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            ps = [PrefillWorkload(dev, hd=hd, tpp=tpp) for _ in range(3)]
+            ms = time_rotated([x.attend for x in ps], max(2, steps // 2), 2, stream)
+            tf = ps[0].flops() / (ms * 1e-3) / 1e12
+            rec["config4_attention"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                                        "frac_of_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
             out[f"hd{hd}_tpp{tpp}"] = rec
-            del ws
+            del ws, ps
             torch.cuda.empty_cache()
     return out
 
