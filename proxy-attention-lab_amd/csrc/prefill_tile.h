@@ -785,7 +785,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // (dims 32n + col) sits kVRowTile slots further
   const int v_base[2] = {IM::v_slot(col, 8 * half), IM::v_slot(col, 16 + 8 * half)};
   // register r holds key k0 + 16 (r/8) + 8 half + 4 ((r/4)%2) + r%4 of
-  // M-row col.  Scores stay raw (the scale is positive, so maxima commute
+  // M-row col (fp8 steps: key k0 + 16 half + r).  Scores stay raw (the scale is positive, so maxima commute
   // with it); the exponent is one fma: s * scale_log2 - m * scale_log2.  The
   // rounding of m * scale_log2 is common to a step's keys and cancels in the
   // normalisation while that product stays below ~2^14 (log2 units; trained
@@ -793,7 +793,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int row0, i
   // exp2 past ~2^31.  An exact (s - m) * scale_log2 costs 16 more VALU
   // instructions per step (a rarely taken branch to it: 3 % on config 4).
   auto mask_score = [&](f32x16& sacc, int r, int st) {
-    const int key = F8 ? st * kKeys + 16 * half + r : st * kKeys + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
+    const int key = F8 ? st * kKeys + 16 * half + r
+                       : st * kKeys + 16 * (r >> 3) + 8 * half + 4 * ((r >> 2) & 1) + (r & 3);
     if (key >= my_lim) sacc[r] = -INFINITY;
   };
   // Given this lane's max bm of a step's scores: moves the running max to the
