@@ -81,7 +81,7 @@ def _decode_case(i):
     return rng, dtype, fp8, hd, tpp, hq, hkv, lens, partition, outliers
 
 
-@pytest.mark.parametrize("i", range(48))
+@pytest.mark.parametrize("i", range(64))
 def test_decode_sweep(i):
     rng, dtype, fp8, hd, tpp, hq, hkv, lens, partition, outliers = _decode_case(i)
     kw = dict(outlier_frac=0.02, outlier_scale=float(rng.choice([4.0, 8.0, 16.0]))) if outliers else {}
@@ -106,7 +106,7 @@ def test_decode_sweep(i):
     assert_close(host_f32(out), ref, dtype, what)
 
 
-@pytest.mark.parametrize("i", range(24))
+@pytest.mark.parametrize("i", range(32))
 def test_prefill_sweep(i):
     rng = np.random.default_rng(3000 + i)
     dtype = "bf16" if rng.random() < 0.6 else "f16"
@@ -129,7 +129,7 @@ def test_prefill_sweep(i):
     assert_close(host_f32(out), ref, dtype, what)
 
 
-@pytest.mark.parametrize("i", range(24))
+@pytest.mark.parametrize("i", range(32))
 def test_fused_sweep(i):
     rng = np.random.default_rng(5000 + i)
     dtype = "bf16" if rng.random() < 0.6 else "f16"
