@@ -82,9 +82,12 @@ def test_fill_random_bit_exact(shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_fill_prefill_chunks_bit_exact(dtype):
-    announce(f"fill consecutive chunks {dtype}")
-    kw = _random_fill_case(5, 4096, 8, 128, 16, 1200, 4, 256, consecutive=True)
+@pytest.mark.parametrize("hd,tpp", [(128, 16), (64, 32), (256, 16), (256, 32)])
+def test_fill_prefill_chunks_bit_exact(dtype, hd, tpp):
+    """Prefill-sized batches (4096 tokens in 4 runs of consecutive positions)
+    take the windowed kernel: every head dim's window size and page size."""
+    announce(f"fill consecutive chunks {dtype} hd={hd} tpp={tpp}")
+    kw = _random_fill_case(5 + hd + tpp, 4096, 8, hd, tpp, 19200 // tpp, 4, 4096 // tpp, consecutive=True)
     _, _, k_out, v_out = _run(kw, dtype)
     ek, ev = orc.fill_kv_pages(**kw)
     assert np.array_equal(host_bits(k_out), ek)
