@@ -181,6 +181,33 @@ def test_rope_fill_head_dims(hd, style, rot_frac):
     assert np.array_equal(host_bits(qo), eq), "rotated queries differ"
 
 
+@pytest.mark.parametrize("hd", [128, 256])
+def test_rope_fill_large_batch(hd):
+    """A prefill-sized RoPE fill (more than 2048 tokens: the 64-token windows,
+    1024 threads per workgroup above head dim 128): pools and rotated queries
+    bit-exact."""
+    hkv, hq, tpp = 4, 8, 16
+    k, v, pt, pos, q2s, _ = fill_layout(hd + 5, hkv, hd, tpp, "bf16", chunks=((0, 1500), (100, 700)))
+    rng = np.random.default_rng(hd + 6)
+    n = len(pos)
+    assert n >= 2048
+    nk = src_values(rng, (n, hkv, hd), "f32", 2.0)
+    nv = src_values(rng, (n, hkv, hd), "f32", 2.0)
+    q = src_values(rng, (n, hq, hd), "f32", 2.0)
+    table = pal.rope_cos_sin_cache(2048, hd, 10000.0, device=DEV)
+    announce(f"rope fill large batch head dim {hd} ({n} tokens)")
+    kd, vd = dev_pool(k, "bf16"), dev_pool(v, "bf16")
+    _, _, qo = pal.rope_fill_kv_pages(dev_f32(nk, "f32"), dev_f32(nv, "f32"), kd, vd, dev_index(pt, torch.uint32),
+                                      dev_index(pos), dev_index(q2s, torch.uint32), table, queries=dev_f32(q, "f32"),
+                                      rotary_dim=hd, style="neox", query_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    ek, ev, eq = orc.fill_kv_pages_ex(nk, nv, k, v, "bf16", pt, pos, q2s, rope=(table.cpu().numpy(), hd, "neox"),
+                                      queries=q, q_out_dtype="bf16")
+    assert np.array_equal(host_pool(kd, "bf16"), ek), "K pool differs"
+    assert np.array_equal(host_pool(vd, "bf16"), ev), "V pool differs"
+    assert np.array_equal(host_bits(qo), eq), "rotated queries differ"
+
+
 def test_rope_fill_positions_outside_table():
     """Tokens whose position has no row in the cos/sin table leave the pools
     alone; their queries come back cast, unrotated."""
